@@ -1,0 +1,213 @@
+/*
+ * ltx25_qlinear.h -- C ABI of the MI355X (gfx950) w8g64 quantized linear
+ * and int8 GEMM tier.
+ *
+ * This is the drop-in boundary for the reference plugin's op vocabulary
+ * (tgo-app-dev/vpipe-ltx-2.5, src/ltx25-metal-ops.h). Each entry point names
+ * the reference interface it replaces. Conventions, all mirroring the
+ * reference's:
+ *
+ *   - Tensors are caller-owned DEVICE pointers (the reference's
+ *     SharedBuffer handles). Nothing here takes ownership.
+ *   - Every op is asynchronous on the caller's stream (a hipStream_t passed
+ *     as `void*`; NULL is the default stream), as the reference's ops only
+ *     ENCODE into the caller's ComputeEncoder and the caller commits and
+ *     waits (src/ltx25-dit.cc:1908-1933).
+ *   - Weights are PyTorch [N out][K in] (src/ltx25-metal-ops.h:80-81);
+ *     activations X are [M][K] bf16, outputs Y are [M][N] bf16, row-major,
+ *     densely packed. Tensors the kernels move as 16-byte vectors (X, Y,
+ *     weights / codes, int8 operands, and the inputs and outputs of the
+ *     elementwise ops) must be 16-byte aligned; a misaligned pointer is
+ *     refused with LTX25_E_INVAL.
+ *   - Return value: LTX25_OK (0) or an LTX25_E_* code; the message for the
+ *     last failure on the calling thread is ltx25_last_error(). This stands
+ *     in for the reference's `std::string* err` out-parameter.
+ *   - Ops that keep scratch (split-K partials, int8 operands) grow it on
+ *     demand and share it across calls, like the reference's `_w_deq` and
+ *     `_i8` scratch (src/ltx25-metal-ops.h:805-809,822-824,843-845): calls
+ *     must be serialised on one stream, as the reference's serial encoder
+ *     serialises them.
+ *
+ * Bias conventions: `bias` is [N] and its element type is `bias_dtype`
+ * (LTX25_DT_NONE with bias == NULL, LTX25_DT_BF16 as in the reference, or
+ * LTX25_DT_F32). In the fused epilogue the bias is added in f32 before the
+ * single rounding to bf16.
+ */
+#ifndef LTX25_QLINEAR_H
+#define LTX25_QLINEAR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- return codes -------------------------------------------------------- */
+#define LTX25_OK 0
+#define LTX25_E_INVAL 1        /* bad argument: null pointer, bad shape       */
+#define LTX25_E_UNSUPPORTED 2  /* well-formed, but no kernel takes it          */
+#define LTX25_E_HIP 3          /* the HIP runtime reported an error            */
+#define LTX25_E_NODEV 4        /* no gfx950 device is visible                  */
+#define LTX25_E_DECLINED 5     /* the int8 tier declined this shape            */
+
+/* ---- element types for bias ------------------------------------------------ */
+#define LTX25_DT_NONE 0
+#define LTX25_DT_BF16 1
+#define LTX25_DT_F32 2
+
+/* ---- fused epilogues -------------------------------------------------------- */
+#define LTX25_EPI_NONE 0
+#define LTX25_EPI_GELU_TANH 1  /* y = gelu_tanh(x.W^T + bias), in f32 */
+
+/* One linear's weight, dense or group-affine quantized.
+ * Replaces `QWeight` (src/ltx25-metal-ops.h:45-57).
+ *   quantized == 0: `w` is bf16 [N][K].
+ *   quantized != 0: `codes` is u32 [N][K*bits/32], LOW bits first (for
+ *   bits == 8 this is exactly little-endian u8 [N][K]); `scales` and
+ *   `qbias` are bf16 [N][K/group]; dequantized w = scale * q + qbias.
+ *   `qbias` is the quantization zero point, NOT the linear's bias. */
+typedef struct ltx25_qweight {
+  const void* w;
+  const void* codes;
+  const void* scales;
+  const void* qbias;
+  int bits;       /* 4 or 8 */
+  int group;      /* 32 or 64 */
+  int quantized;  /* 0 = dense bf16 `w` */
+} ltx25_qweight;
+
+/* ---- lifecycle ------------------------------------------------------------ */
+
+/* Select and check the device (the current HIP device must be gfx950) and
+ * set up kernel attributes. Idempotent. Every compute entry point calls it
+ * on first use.
+ * Replaces MetalOps::init (src/ltx25-metal-ops.h:64). */
+int ltx25_init(void);
+
+/* Message for the last failure on this thread ("" when none). */
+const char* ltx25_last_error(void);
+
+/* 1 when the quantized kernels are available on this device (after a
+ * successful ltx25_init), else 0.
+ * Replaces MetalOps::quant_available (src/ltx25-metal-ops.h:294). */
+int ltx25_quant_available(void);
+
+/* ---- the linear ------------------------------------------------------------- */
+
+/* y[M][N] = x[M][K] . dequant(W)^T (+ bias[N]), bf16 out, f32 accumulate.
+ * A dense weight goes to ltx25_linear. K must be a multiple of the group.
+ * Replaces MetalOps::linear(enc, x, const QWeight&, bias*, y, M, K, N)
+ * (src/ltx25-metal-ops.h:100-105; dispatch at src/ltx25-metal-ops.cc:531-569),
+ * with the bias pass fused into the GEMM epilogue instead of a second
+ * ltx_bias_add dispatch. */
+int ltx25_linear_q(void* stream, const void* x, const ltx25_qweight* w,
+                   const void* bias, int bias_dtype, void* y, int M, int K,
+                   int N);
+
+/* ltx25_linear_q with a fused epilogue (LTX25_EPI_*): the feed-forward's
+ * ff_in + GELU-tanh as one kernel (src/ltx25-block-metal.cc:639-646 issues
+ * them as linear, then gelu). */
+int ltx25_linear_q_ex(void* stream, const void* x, const ltx25_qweight* w,
+                      const void* bias, int bias_dtype, void* y, int M, int K,
+                      int N, int epilogue);
+
+/* Dense bf16 linear: y = x . w^T (+ bias). K must be a multiple of 64.
+ * Replaces the dense MetalOps::linear (src/ltx25-metal-ops.h:82-87;
+ * src/ltx25-metal-ops.cc:504-529). */
+int ltx25_linear(void* stream, const void* x, const void* w_bf16,
+                 const void* bias, int bias_dtype, void* y, int M, int K,
+                 int N);
+
+/* y[M][N] = bf16(f32(y) + f32(bias[n])), in place, bias bf16 or f32.
+ * Replaces MetalOps::bias_add (src/ltx25-metal-ops.h:297-300) and the
+ * ltx_bias_add kernel (src/ltx25-kernels.metal:1420-1441). */
+int ltx25_bias_add(void* stream, void* y, const void* bias, int bias_dtype,
+                   int M, int N);
+
+/* y[i] = bf16(gelu_tanh(f32(x[i]))) over n elements; may run in place.
+ * Replaces MetalOps::gelu / gelu_tanh_ff_f16 (src/ltx25-metal-ops.cc:
+ * 1061-1070; CPU form src/ltx25-block-ref.cc:265-272). */
+int ltx25_gelu_tanh(void* stream, const void* x, void* y, size_t n);
+
+/* Expand a quantized weight to bf16 [N][K]: w = bf16(fma(scale, q, qbias)).
+ * Replaces the dequant-once arm, affine_dequant_w{4,8}g{32,64}
+ * (src/ltx25-metal-ops.cc:467-502). */
+int ltx25_dequant(void* stream, const ltx25_qweight* w, void* out_bf16,
+                  int N, int K);
+
+/* ---- the int8 tier ------------------------------------------------------------ */
+
+/* Turn the int8 tier on (1) or off (0) for ltx25_linear / ltx25_linear_q.
+ * Replaces MetalOps::set_i8_gemm (src/ltx25-metal-ops.h:151). */
+int ltx25_set_i8_gemm(int on);
+
+/* 1 when linear would take the int8 tier for this shape: the tier is on,
+ * M >= 1024, K >= 1024, K % 128 == 0 and N >= 16. Host-only, no device use.
+ * Replaces MetalOps::i8_takes (src/ltx25-metal-ops.h:157; the reference's
+ * gates are asserted at tests/ltx25-i8-gemm-test.cc:144-179). */
+int ltx25_i8_takes(int M, int K, int N);
+
+/* Per-row symmetric int8: scale[m] = absmax_k |x[m][k]| / 127,
+ * q = clamp(rint(x / scale), -127, 127); an all-zero row gives scale 0 and
+ * q 0. Serves activations per token and dense bf16 weights per output
+ * channel. */
+int ltx25_i8_quantize_rows(void* stream, const void* x_bf16, int8_t* q,
+                           float* scale, int M, int K);
+
+/* The same per-output-channel int8 quantization applied to the dequantized
+ * values of a group-affine weight (bf16(fma(scale, q, qbias))), without
+ * materialising the bf16 weight. */
+int ltx25_i8_quantize_qweight(void* stream, const ltx25_qweight* w,
+                              int8_t* wq, float* sw, int N, int K);
+
+/* acc = xq[M][K] . wq[N][K]^T in int32, then
+ * y = bf16(fma(float(acc), sx[m] * sw[n], bias[n] or +0)).
+ * `acc_dbg` (int32 [M][N]) may be NULL; when given, the raw accumulators
+ * are written too (for bit-exact checks). K must be a multiple of 128.
+ * The GEMM under I8GemmContext::gemm (src/ltx25-metal-ops.cc:386-391). */
+int ltx25_i8_gemm(void* stream, const int8_t* xq, const float* sx,
+                  const int8_t* wq, const float* sw, const void* bias,
+                  int bias_dtype, void* y, int32_t* acc_dbg, int M, int K,
+                  int N);
+
+/* ---- packed-weight format ------------------------------------------------------ */
+
+/* u8 codes [N][K] -> u32 words [N][K*bits/32], LOW bits first, and back.
+ * The packing of tests/ltx25-qlinear-test.cc:134-137. */
+int ltx25_pack_codes(void* stream, const uint8_t* q, uint32_t* codes, int N,
+                     int K, int bits);
+int ltx25_unpack_codes(void* stream, const uint32_t* codes, uint8_t* q,
+                       int N, int K, int bits);
+
+/* Group-affine quantize f32 w [N][K] (MLX layout): per group, bias =
+ * bf16(min), scale = bf16((max - min) / (2^bits - 1)),
+ * q = clamp(lround((w - bias) / scale), 0, 2^bits - 1), 0 when scale == 0.
+ * The producer of the packed tensors; restates the quantizer of
+ * tests/ltx25-qlinear-test.cc:93-141 (vpipe's AffineQuantizer is not in the
+ * reference tree). */
+int ltx25_quantize_affine(void* stream, const float* w, void* codes,
+                          void* scales, void* qbias, int N, int K, int bits,
+                          int group);
+
+/* F16 -> bf16 (RNE) of n elements; may run in place. The loader's
+ * conversion of a checkpoint's F16 scales and biases
+ * (src/ltx25-dit-weights.cc:230-278, refill in place at :305-334). */
+int ltx25_f16_to_bf16(void* stream, const void* in_f16, void* out_bf16,
+                      size_t n);
+
+/* Recover bits and group of a packed linear from its tensor shapes, given
+ * the K the architecture says it reads: group = K / scales_cols,
+ * bits = codes_cols * 32 / K (codes counted in u32 words). Returns
+ * LTX25_E_INVAL when the shapes do not close, or when *group is already
+ * set (non-zero) and differs (a checkpoint must use one group size).
+ * Host-only. Replaces need_q_'s shape inference
+ * (src/ltx25-dit-weights.cc:352-403). */
+int ltx25_qweight_infer(int K, long scales_cols, long codes_cols, int* bits,
+                        int* group);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LTX25_QLINEAR_H */

@@ -1,0 +1,119 @@
+"""The C ABI on the host: the library loads, exports every entry point the
+header declares, and its host-only logic (argument validation, the int8
+tier's shape gates, packed-shape inference) behaves as specified without
+touching a device."""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+
+def declared_entry_points():
+    names = set()
+    for f in os.listdir(INCLUDE):
+        if f.endswith(".h"):
+            text = open(os.path.join(INCLUDE, f)).read()
+            names |= set(re.findall(r"^\s*(?:int|const char\*|void)\s+(ltx25_\w+)\s*\(", text,
+                                    re.M))
+    return sorted(names)
+
+
+def test_header_declares_the_boundary():
+    names = declared_entry_points()
+    for must in ["ltx25_init", "ltx25_linear_q", "ltx25_linear", "ltx25_bias_add",
+                 "ltx25_set_i8_gemm", "ltx25_i8_takes", "ltx25_i8_gemm",
+                 "ltx25_quant_available", "ltx25_last_error"]:
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_entry_points():
+        assert hasattr(lib, name), f"{name} is declared but not exported"
+
+
+def test_binding_covers_every_declared_symbol(pkg):
+    assert set(declared_entry_points()) == set(pkg.SIGNATURES)
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device path")
+def test_init_without_a_device_reports_nodev(pkg, lib):
+    assert lib.ltx25_init() == pkg.E_NODEV
+    assert pkg.last_error()
+    assert lib.ltx25_quant_available() == 0
+
+
+def test_validation_precedes_any_device_use(pkg, lib):
+    fake = 0x1000  # never dereferenced: every call below fails validation first
+    q = pkg.QWeightC(None, fake, fake, fake, 8, 64, 1)
+    import ctypes
+
+    def call(M, K, N, w=q, bias=None, dt=pkg.DT_NONE, epi=0):
+        return lib.ltx25_linear_q_ex(None, fake, ctypes.byref(w), bias, dt, fake, M, K, N, epi)
+
+    assert call(16, 100, 128) == pkg.E_INVAL                  # K not a multiple of group
+    assert "group" in pkg.last_error()
+    assert call(0, 256, 128) == pkg.E_INVAL
+    assert call(16, 256, 128, bias=fake, dt=pkg.DT_NONE) == pkg.E_INVAL
+    assert call(16, 256, 128, epi=7) == pkg.E_INVAL
+    bad_bits = pkg.QWeightC(None, fake, fake, fake, 5, 64, 1)
+    assert call(16, 256, 128, w=bad_bits) == pkg.E_INVAL
+    bad_group = pkg.QWeightC(None, fake, fake, fake, 8, 48, 1)
+    assert call(16, 192, 128, w=bad_group) == pkg.E_INVAL
+    no_codes = pkg.QWeightC(None, None, fake, fake, 8, 64, 1)
+    assert call(16, 256, 128, w=no_codes) == pkg.E_INVAL
+    # dense K=81 (the reference's VAE conv_in) is well-formed but no kernel takes it
+    assert lib.ltx25_linear(None, fake, fake, None, 0, fake, 4096, 81, 128) == pkg.E_UNSUPPORTED
+    assert lib.ltx25_i8_gemm(None, fake, fake, fake, fake, None, 0, fake, None, 64, 100,
+                             64) == pkg.E_UNSUPPORTED
+    assert lib.ltx25_pack_codes(None, fake, fake, 4, 6, 8) == pkg.E_INVAL  # 6 codes != words
+
+
+def test_i8_takes_gates(pkg):
+    pkg.set_i8_gemm(False)
+    assert not pkg.i8_takes(8160, 4096, 4096)
+    pkg.set_i8_gemm(True)
+    try:
+        # the DiT's projections at a clip's token count (tests/ltx25-i8-gemm-test.cc:155-161)
+        assert pkg.i8_takes(8160, 4096, 4096)
+        assert pkg.i8_takes(8160, 4096, 16384)
+        assert pkg.i8_takes(8160, 16384, 4096)
+        assert pkg.i8_takes(8160, 3840, 4096)
+        # refused: short M, shallow K (tests/ltx25-i8-gemm-test.cc:164-165)
+        assert not pkg.i8_takes(512, 4096, 4096)
+        assert not pkg.i8_takes(8160, 512, 4096)
+        assert not pkg.i8_takes(8160, 1000, 4096)       # K not a multiple of 128
+        assert not pkg.i8_takes(8160, 4096, 8)          # narrow N
+    finally:
+        pkg.set_i8_gemm(False)
+
+
+def test_qweight_infer_recovers_bits_and_group(pkg):
+    # K = 4096: w8g64 packs 1024 u32 words and 64 scale columns per row
+    assert pkg.qweight_infer(4096, 64, 1024) == (8, 64)
+    assert pkg.qweight_infer(4096, 128, 512) == (4, 32)
+    assert pkg.qweight_infer(4096, 64, 512) == (4, 64)
+    assert pkg.qweight_infer(2048, 64, 512, group=32) == (8, 32)
+    with pytest.raises(pkg.Ltx25Error):
+        pkg.qweight_infer(4096, 64, 1000)                # codes do not close
+    with pytest.raises(pkg.Ltx25Error):
+        pkg.qweight_infer(4096, 100, 1024)               # group not 32/64
+    with pytest.raises(pkg.Ltx25Error):
+        pkg.qweight_infer(4096, 128, 1024, group=64)     # second group size in one pack
+
+
+def test_cpp_facade_compiles():
+    cxx = shutil.which("g++")
+    if cxx is None:
+        pytest.skip("no host C++ compiler")
+    src = "#include \"ltx25_ops.h\"\nint main(){ ltx25::Ops o; ltx25::QWeight w; return w.empty() ? 0 : 1; }\n"
+    r = subprocess.run([cxx, "-std=c++17", "-fsyntax-only", "-x", "c++", "-",
+                        "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", "-I" + INCLUDE,
+                        "-I" + os.path.join(ROOT, "vpipe-ltx-2.5_amd", "csrc")],
+                       input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]

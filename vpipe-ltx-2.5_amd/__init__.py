@@ -1,0 +1,230 @@
+"""Python binding of the ltx25 quantized-linear C ABI (include/ltx25_qlinear.h).
+
+A thin ctypes layer over libltx25_qlinear.so for tests and the benchmark:
+device buffers are torch tensors (plumbing only) whose data pointers are
+passed through the C ABI, and every call runs on torch's current stream
+unless a stream is given. The HIP library is the only compute path; when it
+is missing, load() raises instead of falling back to anything else.
+
+The package directory name is not a Python identifier, so callers import it
+by path; ``load_package()`` in __graft_entry__.py and tests/conftest.py do
+that.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libltx25_qlinear.so")
+HEADER_PATH = os.path.join(HERE, "..", "include", "ltx25_qlinear.h")
+
+OK = 0
+E_INVAL = 1
+E_UNSUPPORTED = 2
+E_HIP = 3
+E_NODEV = 4
+E_DECLINED = 5
+
+DT_NONE = 0
+DT_BF16 = 1
+DT_F32 = 2
+
+EPI_NONE = 0
+EPI_GELU_TANH = 1
+
+
+class QWeightC(ctypes.Structure):
+    """ltx25_qweight (mirrors QWeight, src/ltx25-metal-ops.h:45-57)."""
+
+    _fields_ = [
+        ("w", ctypes.c_void_p),
+        ("codes", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("qbias", ctypes.c_void_p),
+        ("bits", ctypes.c_int),
+        ("group", ctypes.c_int),
+        ("quantized", ctypes.c_int),
+    ]
+
+
+class Ltx25Error(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"ltx25 error {code}: {msg}")
+        self.code = code
+
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_sz = ctypes.c_size_t
+_long = ctypes.c_long
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "ltx25_init": (_i, []),
+    "ltx25_last_error": (ctypes.c_char_p, []),
+    "ltx25_quant_available": (_i, []),
+    "ltx25_linear_q": (_i, [_vp, _vp, ctypes.POINTER(QWeightC), _vp, _i, _vp, _i, _i, _i]),
+    "ltx25_linear_q_ex": (_i, [_vp, _vp, ctypes.POINTER(QWeightC), _vp, _i, _vp, _i, _i, _i, _i]),
+    "ltx25_linear": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i]),
+    "ltx25_bias_add": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "ltx25_gelu_tanh": (_i, [_vp, _vp, _vp, _sz]),
+    "ltx25_dequant": (_i, [_vp, ctypes.POINTER(QWeightC), _vp, _i, _i]),
+    "ltx25_set_i8_gemm": (_i, [_i]),
+    "ltx25_i8_takes": (_i, [_i, _i, _i]),
+    "ltx25_i8_quantize_rows": (_i, [_vp, _vp, _vp, _vp, _i, _i]),
+    "ltx25_i8_quantize_qweight": (_i, [_vp, ctypes.POINTER(QWeightC), _vp, _vp, _i, _i]),
+    "ltx25_i8_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i]),
+    "ltx25_pack_codes": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "ltx25_unpack_codes": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "ltx25_quantize_affine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i]),
+    "ltx25_f16_to_bf16": (_i, [_vp, _vp, _vp, _sz]),
+    "ltx25_qweight_infer": (_i, [_i, _long, _long, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libltx25_qlinear.so once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(
+            f"{path} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')"
+        )
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().ltx25_last_error().decode()
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        raise Ltx25Error(rc, last_error())
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is not None:
+        return stream
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def bias_dtype_of(bias) -> int:
+    if bias is None:
+        return DT_NONE
+    import torch
+
+    if bias.dtype == torch.bfloat16:
+        return DT_BF16
+    if bias.dtype == torch.float32:
+        return DT_F32
+    raise TypeError(f"bias must be bf16 or f32, got {bias.dtype}")
+
+
+class QWeight:
+    """A packed linear weight held in torch device tensors.
+
+    codes: uint8 [N][K*bits/8] (the little-endian bytes of the u32 words),
+    scales / qbias: bf16 [N][K/group].
+    """
+
+    def __init__(self, codes, scales, qbias, bits: int = 8, group: int = 64):
+        self.codes, self.scales, self.qbias = codes, scales, qbias
+        self.bits, self.group = bits, group
+
+    def c(self) -> QWeightC:
+        return QWeightC(None, _ptr(self.codes), _ptr(self.scales), _ptr(self.qbias),
+                        self.bits, self.group, 1)
+
+
+def dense_weight(w) -> QWeightC:
+    return QWeightC(_ptr(w), None, None, None, 0, 0, 0)
+
+
+def linear_q(x, w: QWeight, bias, y, M: int, K: int, N: int, epilogue: int = EPI_NONE,
+             stream=None) -> None:
+    cw = w.c()
+    check(load().ltx25_linear_q_ex(_stream(stream), _ptr(x), ctypes.byref(cw), _ptr(bias),
+                                   bias_dtype_of(bias), _ptr(y), M, K, N, epilogue))
+
+
+def linear(x, w, bias, y, M: int, K: int, N: int, stream=None) -> None:
+    check(load().ltx25_linear(_stream(stream), _ptr(x), _ptr(w), _ptr(bias),
+                              bias_dtype_of(bias), _ptr(y), M, K, N))
+
+
+def bias_add(y, bias, M: int, N: int, stream=None) -> None:
+    check(load().ltx25_bias_add(_stream(stream), _ptr(y), _ptr(bias), bias_dtype_of(bias), M, N))
+
+
+def gelu_tanh(x, y, stream=None) -> None:
+    check(load().ltx25_gelu_tanh(_stream(stream), _ptr(x), _ptr(y), x.numel()))
+
+
+def dequant(w: QWeight, out, N: int, K: int, stream=None) -> None:
+    cw = w.c()
+    check(load().ltx25_dequant(_stream(stream), ctypes.byref(cw), _ptr(out), N, K))
+
+
+def quantize_affine(w_f32, codes, scales, qbias, N: int, K: int, bits: int = 8,
+                    group: int = 64, stream=None) -> None:
+    check(load().ltx25_quantize_affine(_stream(stream), _ptr(w_f32), _ptr(codes), _ptr(scales),
+                                       _ptr(qbias), N, K, bits, group))
+
+
+def pack_codes(q, codes, N: int, K: int, bits: int, stream=None) -> None:
+    check(load().ltx25_pack_codes(_stream(stream), _ptr(q), _ptr(codes), N, K, bits))
+
+
+def unpack_codes(codes, q, N: int, K: int, bits: int, stream=None) -> None:
+    check(load().ltx25_unpack_codes(_stream(stream), _ptr(codes), _ptr(q), N, K, bits))
+
+
+def f16_to_bf16(src, dst, stream=None) -> None:
+    check(load().ltx25_f16_to_bf16(_stream(stream), _ptr(src), _ptr(dst), src.numel()))
+
+
+def set_i8_gemm(on: bool) -> None:
+    check(load().ltx25_set_i8_gemm(1 if on else 0))
+
+
+def i8_takes(M: int, K: int, N: int) -> bool:
+    return bool(load().ltx25_i8_takes(M, K, N))
+
+
+def i8_quantize_rows(x, q, scale, M: int, K: int, stream=None) -> None:
+    check(load().ltx25_i8_quantize_rows(_stream(stream), _ptr(x), _ptr(q), _ptr(scale), M, K))
+
+
+def i8_quantize_qweight(w: QWeight, wq, sw, N: int, K: int, stream=None) -> None:
+    cw = w.c()
+    check(load().ltx25_i8_quantize_qweight(_stream(stream), ctypes.byref(cw), _ptr(wq), _ptr(sw),
+                                           N, K))
+
+
+def i8_gemm(xq, sx, wq, sw, bias, y, acc, M: int, K: int, N: int, stream=None) -> None:
+    check(load().ltx25_i8_gemm(_stream(stream), _ptr(xq), _ptr(sx), _ptr(wq), _ptr(sw),
+                               _ptr(bias), bias_dtype_of(bias), _ptr(y), _ptr(acc), M, K, N))
+
+
+def qweight_infer(K: int, scales_cols: int, codes_cols: int, group: int = 0) -> tuple[int, int]:
+    """(bits, group) from packed shapes; raises Ltx25Error when they do not close."""
+    b = ctypes.c_int(0)
+    g = ctypes.c_int(group)
+    check(load().ltx25_qweight_infer(K, scales_cols, codes_cols, ctypes.byref(b), ctypes.byref(g)))
+    return b.value, g.value

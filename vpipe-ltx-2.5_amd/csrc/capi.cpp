@@ -1,0 +1,540 @@
+// The C ABI (include/ltx25_qlinear.h): argument validation, the dispatch
+// policy between the tile shapes / split-K / int8 tier, and the grow-only
+// scratch the split-K and int8 paths share.
+//
+// Validation runs before any HIP call, so malformed calls fail the same
+// way on a host without a GPU. The reference reports shape errors at bind
+// time and asserts in `linear`; here every entry point returns a code and
+// leaves the message in ltx25_last_error().
+#include "ltx25_qlinear.h"
+
+#include "common.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...)
+{
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what)
+{
+  return fail(LTX25_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int kMaxDevices = 64;
+
+// Per-device state: checked once, then the grow-only scratch.
+struct DeviceState {
+  bool checked = false;
+  bool ok = false;
+  int cu_count = 0;
+  char arch[64] = {0};
+  void* ws = nullptr;        // split-K f32 partials
+  size_t ws_bytes = 0;
+  void* i8 = nullptr;        // int8 tier operands: xq | sx | wq | sw
+  size_t i8_bytes = 0;
+};
+
+std::mutex g_mu;
+DeviceState g_dev[kMaxDevices];
+int g_i8_on = 0;
+
+// Check (once per device) that the current device is gfx950.
+int current_device(DeviceState** out)
+{
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0) {
+    int count = 0;
+    (void)hipGetDeviceCount(&count);
+    return fail(LTX25_E_NODEV, "no HIP device is visible (%s)",
+                hipGetErrorString(e));
+  }
+  if (dev >= kMaxDevices) {
+    return fail(LTX25_E_NODEV, "device index %d is out of range", dev);
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState& s = g_dev[dev];
+  if (!s.checked) {
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) { return hip_fail(e, "hipGetDeviceProperties"); }
+    std::snprintf(s.arch, sizeof s.arch, "%s", prop.gcnArchName);
+    s.cu_count = prop.multiProcessorCount;
+    s.ok = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    s.checked = true;
+  }
+  if (!s.ok) {
+    return fail(LTX25_E_NODEV,
+                "device %d is %s; these kernels are built for gfx950 only",
+                dev, s.arch);
+  }
+  *out = &s;
+  return LTX25_OK;
+}
+
+// Grow `*buf` to at least `need` bytes. The old buffer may still be read by
+// work queued earlier, so the device is drained before it is released.
+int grow(void** buf, size_t* cap, size_t need)
+{
+  if (*cap >= need) { return LTX25_OK; }
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) { return hip_fail(e, "hipDeviceSynchronize"); }
+  if (*buf != nullptr) {
+    (void)hipFree(*buf);
+    *buf = nullptr;
+    *cap = 0;
+  }
+  e = hipMalloc(buf, need);
+  if (e != hipSuccess) {
+    *buf = nullptr;
+    return hip_fail(e, "hipMalloc (scratch)");
+  }
+  *cap = need;
+  return LTX25_OK;
+}
+
+// The kernels move 16-byte vectors, so every tensor base must be 16-byte
+// aligned (any allocator's base pointer is; a sliced view may not be).
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_aligned(const char* what, const void* p)
+{
+  if (p != nullptr && !aligned16(p)) {
+    return fail(LTX25_E_INVAL, "%s (%p) is not 16-byte aligned", what, p);
+  }
+  return LTX25_OK;
+}
+
+bool bias_ok(const void* bias, int dt)
+{
+  if (bias == nullptr) { return dt == LTX25_DT_NONE || dt == LTX25_DT_BF16 || dt == LTX25_DT_F32; }
+  return dt == LTX25_DT_BF16 || dt == LTX25_DT_F32;
+}
+
+int check_shape(int M, int K, int N)
+{
+  if (M <= 0 || K <= 0 || N <= 0) {
+    return fail(LTX25_E_INVAL, "shape M=%d K=%d N=%d must be positive", M, K, N);
+  }
+  return LTX25_OK;
+}
+
+int check_qweight(const ltx25_qweight* w, int K)
+{
+  if (w == nullptr) { return fail(LTX25_E_INVAL, "weight is null"); }
+  if (!w->quantized) {
+    if (w->w == nullptr) { return fail(LTX25_E_INVAL, "dense weight `w` is null"); }
+    return LTX25_OK;
+  }
+  if (w->codes == nullptr || w->scales == nullptr || w->qbias == nullptr) {
+    return fail(LTX25_E_INVAL, "quantized weight has a null codes/scales/qbias");
+  }
+  if (w->bits != 8 && w->bits != 4) {
+    return fail(LTX25_E_INVAL, "bits=%d; only 4 and 8 are packed", w->bits);
+  }
+  if (w->group != 64 && w->group != 32) {
+    return fail(LTX25_E_INVAL, "group=%d; only 32 and 64 are packed", w->group);
+  }
+  if (K % w->group != 0) {
+    return fail(LTX25_E_INVAL, "K=%d is not a multiple of the group %d", K, w->group);
+  }
+  return LTX25_OK;
+}
+
+int run_i8_linear(DeviceState* ds, hipStream_t st, const void* x,
+                  const ltx25_qweight* w, const void* bias, int bias_dtype,
+                  void* y, int M, int K, int N);
+
+int run_linear(hipStream_t st, const void* x, const ltx25_qweight* w,
+               const void* bias, int bias_dtype, void* y, int M, int K, int N,
+               int epilogue)
+{
+  if (x == nullptr || y == nullptr) { return fail(LTX25_E_INVAL, "x or y is null"); }
+  int rc = check_shape(M, K, N);
+  if (rc != LTX25_OK) { return rc; }
+  rc = check_qweight(w, K);
+  if (rc != LTX25_OK) { return rc; }
+  if (!bias_ok(bias, bias_dtype)) {
+    return fail(LTX25_E_INVAL, "bias dtype %d is not valid for a %s bias",
+                bias_dtype, bias == nullptr ? "null" : "non-null");
+  }
+  if (epilogue != LTX25_EPI_NONE && epilogue != LTX25_EPI_GELU_TANH) {
+    return fail(LTX25_E_INVAL, "unknown epilogue %d", epilogue);
+  }
+  if ((rc = check_aligned("x", x)) != LTX25_OK || (rc = check_aligned("y", y)) != LTX25_OK ||
+      (rc = check_aligned("weight", w->quantized ? w->codes : w->w)) != LTX25_OK) {
+    return rc;
+  }
+  if (K % 64 != 0) {
+    return fail(LTX25_E_UNSUPPORTED,
+                "K=%d: the MFMA kernels step K by 64; pad K to a multiple of 64", K);
+  }
+  DeviceState* ds = nullptr;
+  rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+
+  if (epilogue == LTX25_EPI_NONE && ltx25_i8_takes(M, K, N)) {
+    return run_i8_linear(ds, st, x, w, bias, bias_dtype, y, M, K, N);
+  }
+
+  ltx25::GemmDesc d;
+  d.x = (const uint16_t*)x;
+  d.w = w->quantized ? w->codes : w->w;
+  d.scales = (const uint16_t*)w->scales;
+  d.qbias = (const uint16_t*)w->qbias;
+  d.bits = w->quantized ? w->bits : 16;
+  d.group = w->quantized ? w->group : 64;
+  d.bias = bias;
+  d.bias_type = bias != nullptr ? bias_dtype : ltx25::kBiasNone;
+  d.epilogue = epilogue;
+  d.y = (uint16_t*)y;
+  d.M = M;
+  d.N = N;
+  d.K = K;
+  const ltx25::GemmPlan plan = ltx25::plan_gemm(M, N, K, ds->cu_count);
+  float* ws = nullptr;
+  if (plan.workspace_bytes > 0) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    rc = grow(&ds->ws, &ds->ws_bytes, plan.workspace_bytes);
+    if (rc != LTX25_OK) { return rc; }
+    ws = (float*)ds->ws;
+  }
+  const hipError_t e = ltx25::launch_gemm(d, plan, ws, st);
+  if (e != hipSuccess) { return hip_fail(e, "qgemm launch"); }
+  return LTX25_OK;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// The int8 tier inside `linear`: quantize the activation per token and the
+// weight per output channel for THIS call (the reference's tier keeps no
+// persistent weight copy either, src/ltx25-metal-ops.h:810-816), then the
+// int8 GEMM with the fused dequant epilogue.
+int run_i8_linear(DeviceState* ds, hipStream_t st, const void* x,
+                  const ltx25_qweight* w, const void* bias, int bias_dtype,
+                  void* y, int M, int K, int N)
+{
+  const size_t xq_b = align256((size_t)M * K);
+  const size_t sx_b = align256((size_t)M * 4);
+  const size_t wq_b = align256((size_t)N * K);
+  const size_t sw_b = align256((size_t)N * 4);
+  char* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const int rc = grow(&ds->i8, &ds->i8_bytes, xq_b + sx_b + wq_b + sw_b);
+    if (rc != LTX25_OK) { return rc; }
+    base = (char*)ds->i8;
+  }
+  int8_t* xq = (int8_t*)base;
+  float* sx = (float*)(base + xq_b);
+  int8_t* wq = (int8_t*)(base + xq_b + sx_b);
+  float* sw = (float*)(base + xq_b + sx_b + wq_b);
+  hipError_t e = ltx25::launch_i8_quantize_rows((const uint16_t*)x, xq, sx, M, K, st);
+  if (e != hipSuccess) { return hip_fail(e, "i8 quantize (x)"); }
+  if (w->quantized) {
+    e = ltx25::launch_i8_quantize_qweight(w->codes, (const uint16_t*)w->scales,
+                                          (const uint16_t*)w->qbias, w->bits,
+                                          w->group, wq, sw, N, K, st);
+  } else {
+    e = ltx25::launch_i8_quantize_rows((const uint16_t*)w->w, wq, sw, N, K, st);
+  }
+  if (e != hipSuccess) { return hip_fail(e, "i8 quantize (w)"); }
+  e = ltx25::launch_i8_gemm(xq, sx, wq, sw, bias, bias != nullptr ? bias_dtype : 0,
+                            (uint16_t*)y, nullptr, M, K, N, st);
+  if (e != hipSuccess) { return hip_fail(e, "i8 gemm launch"); }
+  return LTX25_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ltx25_init(void)
+{
+  DeviceState* ds = nullptr;
+  return current_device(&ds);
+}
+
+const char* ltx25_last_error(void) { return g_err.c_str(); }
+
+int ltx25_quant_available(void)
+{
+  DeviceState* ds = nullptr;
+  return current_device(&ds) == LTX25_OK ? 1 : 0;
+}
+
+int ltx25_linear_q(void* stream, const void* x, const ltx25_qweight* w,
+                   const void* bias, int bias_dtype, void* y, int M, int K,
+                   int N)
+{
+  return run_linear((hipStream_t)stream, x, w, bias, bias_dtype, y, M, K, N,
+                    LTX25_EPI_NONE);
+}
+
+int ltx25_linear_q_ex(void* stream, const void* x, const ltx25_qweight* w,
+                      const void* bias, int bias_dtype, void* y, int M, int K,
+                      int N, int epilogue)
+{
+  return run_linear((hipStream_t)stream, x, w, bias, bias_dtype, y, M, K, N,
+                    epilogue);
+}
+
+int ltx25_linear(void* stream, const void* x, const void* w_bf16,
+                 const void* bias, int bias_dtype, void* y, int M, int K,
+                 int N)
+{
+  ltx25_qweight w;
+  std::memset(&w, 0, sizeof w);
+  w.w = w_bf16;
+  w.quantized = 0;
+  return run_linear((hipStream_t)stream, x, &w, bias, bias_dtype, y, M, K, N,
+                    LTX25_EPI_NONE);
+}
+
+int ltx25_bias_add(void* stream, void* y, const void* bias, int bias_dtype,
+                   int M, int N)
+{
+  if (y == nullptr || bias == nullptr) { return fail(LTX25_E_INVAL, "y or bias is null"); }
+  if (bias_dtype != LTX25_DT_BF16 && bias_dtype != LTX25_DT_F32) {
+    return fail(LTX25_E_INVAL, "bias dtype %d is not bf16 or f32", bias_dtype);
+  }
+  if (M <= 0 || N <= 0) { return fail(LTX25_E_INVAL, "M=%d N=%d must be positive", M, N); }
+  if (check_aligned("y", y) != LTX25_OK) { return LTX25_E_INVAL; }
+  DeviceState* ds = nullptr;
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_bias_add((uint16_t*)y, bias, bias_dtype, M, N,
+                                              (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "bias_add launch");
+}
+
+int ltx25_gelu_tanh(void* stream, const void* x, void* y, size_t n)
+{
+  if (x == nullptr || y == nullptr) { return fail(LTX25_E_INVAL, "x or y is null"); }
+  if (n == 0) { return LTX25_OK; }
+  if (check_aligned("x", x) != LTX25_OK || check_aligned("y", y) != LTX25_OK) {
+    return LTX25_E_INVAL;
+  }
+  DeviceState* ds = nullptr;
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_gelu((const uint16_t*)x, (uint16_t*)y, n,
+                                          (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "gelu launch");
+}
+
+int ltx25_dequant(void* stream, const ltx25_qweight* w, void* out_bf16, int N,
+                  int K)
+{
+  if (out_bf16 == nullptr) { return fail(LTX25_E_INVAL, "out is null"); }
+  if (N <= 0 || K <= 0) { return fail(LTX25_E_INVAL, "N=%d K=%d must be positive", N, K); }
+  int rc = check_qweight(w, K);
+  if (rc != LTX25_OK) { return rc; }
+  if (!w->quantized) { return fail(LTX25_E_INVAL, "dequant needs a quantized weight"); }
+  if ((rc = check_aligned("codes", w->codes)) != LTX25_OK ||
+      (rc = check_aligned("out", out_bf16)) != LTX25_OK) {
+    return rc;
+  }
+  DeviceState* ds = nullptr;
+  rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_dequant(w->codes, (const uint16_t*)w->scales,
+                                             (const uint16_t*)w->qbias, w->bits,
+                                             w->group, (uint16_t*)out_bf16, N, K,
+                                             (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "dequant launch");
+}
+
+int ltx25_set_i8_gemm(int on)
+{
+  g_i8_on = on != 0;
+  return LTX25_OK;
+}
+
+int ltx25_i8_takes(int M, int K, int N)
+{
+  return g_i8_on && M >= 1024 && K >= 1024 && K % 128 == 0 && N >= 16 ? 1 : 0;
+}
+
+int ltx25_i8_quantize_rows(void* stream, const void* x_bf16, int8_t* q,
+                           float* scale, int M, int K)
+{
+  if (x_bf16 == nullptr || q == nullptr || scale == nullptr) {
+    return fail(LTX25_E_INVAL, "null pointer");
+  }
+  if (M <= 0 || K <= 0) { return fail(LTX25_E_INVAL, "M=%d K=%d must be positive", M, K); }
+  if (K % 8 != 0) { return fail(LTX25_E_UNSUPPORTED, "K=%d is not a multiple of 8", K); }
+  if (check_aligned("x", x_bf16) != LTX25_OK || check_aligned("q", q) != LTX25_OK) {
+    return LTX25_E_INVAL;
+  }
+  DeviceState* ds = nullptr;
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_i8_quantize_rows((const uint16_t*)x_bf16, q, scale,
+                                                      M, K, (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "i8 quantize launch");
+}
+
+int ltx25_i8_quantize_qweight(void* stream, const ltx25_qweight* w,
+                              int8_t* wq, float* sw, int N, int K)
+{
+  if (wq == nullptr || sw == nullptr) { return fail(LTX25_E_INVAL, "null pointer"); }
+  if (N <= 0 || K <= 0) { return fail(LTX25_E_INVAL, "N=%d K=%d must be positive", N, K); }
+  int rc = check_qweight(w, K);
+  if (rc != LTX25_OK) { return rc; }
+  DeviceState* ds = nullptr;
+  rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  hipError_t e;
+  if (w->quantized) {
+    e = ltx25::launch_i8_quantize_qweight(w->codes, (const uint16_t*)w->scales,
+                                          (const uint16_t*)w->qbias, w->bits, w->group,
+                                          wq, sw, N, K, (hipStream_t)stream);
+  } else {
+    if (K % 8 != 0) { return fail(LTX25_E_UNSUPPORTED, "K=%d is not a multiple of 8", K); }
+    if (check_aligned("w", w->w) != LTX25_OK || check_aligned("wq", wq) != LTX25_OK) {
+      return LTX25_E_INVAL;
+    }
+    e = ltx25::launch_i8_quantize_rows((const uint16_t*)w->w, wq, sw, N, K,
+                                       (hipStream_t)stream);
+  }
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "i8 weight quantize launch");
+}
+
+int ltx25_i8_gemm(void* stream, const int8_t* xq, const float* sx,
+                  const int8_t* wq, const float* sw, const void* bias,
+                  int bias_dtype, void* y, int32_t* acc_dbg, int M, int K,
+                  int N)
+{
+  if (xq == nullptr || sx == nullptr || wq == nullptr || sw == nullptr || y == nullptr) {
+    return fail(LTX25_E_INVAL, "null pointer");
+  }
+  int rc = check_shape(M, K, N);
+  if (rc != LTX25_OK) { return rc; }
+  if (!bias_ok(bias, bias_dtype)) { return fail(LTX25_E_INVAL, "bad bias dtype %d", bias_dtype); }
+  if (K % 128 != 0) {
+    return fail(LTX25_E_UNSUPPORTED, "K=%d: the int8 MFMA kernel steps K by 128", K);
+  }
+  if ((rc = check_aligned("xq", xq)) != LTX25_OK || (rc = check_aligned("wq", wq)) != LTX25_OK) {
+    return rc;
+  }
+  DeviceState* ds = nullptr;
+  rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_i8_gemm(xq, sx, wq, sw, bias,
+                                             bias != nullptr ? bias_dtype : 0,
+                                             (uint16_t*)y, acc_dbg, M, K, N,
+                                             (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "i8 gemm launch");
+}
+
+int ltx25_pack_codes(void* stream, const uint8_t* q, uint32_t* codes, int N,
+                     int K, int bits)
+{
+  if (q == nullptr || codes == nullptr) { return fail(LTX25_E_INVAL, "null pointer"); }
+  if (N <= 0 || K <= 0) { return fail(LTX25_E_INVAL, "N=%d K=%d must be positive", N, K); }
+  if ((bits != 4 && bits != 8) || ((long)K * bits) % 32 != 0) {
+    return fail(LTX25_E_INVAL, "bits=%d K=%d do not fill whole u32 words", bits, K);
+  }
+  DeviceState* ds = nullptr;
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_pack(q, codes, N, K, bits, (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "pack launch");
+}
+
+int ltx25_unpack_codes(void* stream, const uint32_t* codes, uint8_t* q,
+                       int N, int K, int bits)
+{
+  if (q == nullptr || codes == nullptr) { return fail(LTX25_E_INVAL, "null pointer"); }
+  if (N <= 0 || K <= 0) { return fail(LTX25_E_INVAL, "N=%d K=%d must be positive", N, K); }
+  if ((bits != 4 && bits != 8) || ((long)K * bits) % 32 != 0) {
+    return fail(LTX25_E_INVAL, "bits=%d K=%d do not fill whole u32 words", bits, K);
+  }
+  DeviceState* ds = nullptr;
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_unpack(codes, q, N, K, bits, (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "unpack launch");
+}
+
+int ltx25_quantize_affine(void* stream, const float* w, void* codes,
+                          void* scales, void* qbias, int N, int K, int bits,
+                          int group)
+{
+  if (w == nullptr || codes == nullptr || scales == nullptr || qbias == nullptr) {
+    return fail(LTX25_E_INVAL, "null pointer");
+  }
+  if (N <= 0 || K <= 0) { return fail(LTX25_E_INVAL, "N=%d K=%d must be positive", N, K); }
+  if (bits != 4 && bits != 8) { return fail(LTX25_E_INVAL, "bits=%d; only 4 and 8", bits); }
+  if (group != 32 && group != 64) { return fail(LTX25_E_INVAL, "group=%d; only 32 and 64", group); }
+  if (K % group != 0) { return fail(LTX25_E_INVAL, "K=%d is not a multiple of group %d", K, group); }
+  DeviceState* ds = nullptr;
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_quantize_affine(w, (uint32_t*)codes, (uint16_t*)scales,
+                                                     (uint16_t*)qbias, N, K, bits, group,
+                                                     (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "quantize launch");
+}
+
+int ltx25_f16_to_bf16(void* stream, const void* in_f16, void* out_bf16,
+                      size_t n)
+{
+  if (in_f16 == nullptr || out_bf16 == nullptr) { return fail(LTX25_E_INVAL, "null pointer"); }
+  if (n == 0) { return LTX25_OK; }
+  if (check_aligned("in", in_f16) != LTX25_OK || check_aligned("out", out_bf16) != LTX25_OK) {
+    return LTX25_E_INVAL;
+  }
+  DeviceState* ds = nullptr;
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_f16_to_bf16((const uint16_t*)in_f16, (uint16_t*)out_bf16,
+                                                 n, (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "f16_to_bf16 launch");
+}
+
+int ltx25_qweight_infer(int K, long scales_cols, long codes_cols, int* bits,
+                        int* group)
+{
+  if (bits == nullptr || group == nullptr) { return fail(LTX25_E_INVAL, "null out-pointer"); }
+  if (K <= 0 || scales_cols <= 0 || codes_cols <= 0) {
+    return fail(LTX25_E_INVAL, "K=%d, scales cols=%ld, codes cols=%ld must be positive",
+                K, scales_cols, codes_cols);
+  }
+  const long g = (long)K / scales_cols;
+  const long b = codes_cols * 32 / (long)K;
+  if ((g != 32 && g != 64) || (b != 4 && b != 8) || scales_cols * g != (long)K ||
+      codes_cols * 32 != (long)K * b) {
+    return fail(LTX25_E_INVAL,
+                "shapes do not close: K=%d, scales cols=%ld, codes cols=%ld", K,
+                scales_cols, codes_cols);
+  }
+  if (*group != 0 && *group != (int)g) {
+    return fail(LTX25_E_INVAL, "packed at group %ld but the checkpoint already used group %d",
+                g, *group);
+  }
+  *group = (int)g;
+  *bits = (int)b;
+  return LTX25_OK;
+}
+
+}  // extern "C"

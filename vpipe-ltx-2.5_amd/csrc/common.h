@@ -1,0 +1,112 @@
+// Device-side helpers shared by the gfx950 kernels, and the internal
+// launcher interface between the kernels and the C ABI layer (capi.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace ltx25 {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h)
+{
+  return __uint_as_float((uint32_t)h << 16);
+}
+
+// Two floats -> two bf16 (round to nearest even) in one v_cvt_pk_bf16_f32,
+// `lo` in the low half.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
+{
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f)
+{
+  return (uint16_t)(pack_bf16x2(f, 0.0f) & 0xffffu);
+}
+
+// GELU, tanh approximation: 0.5 x (1 + tanh(u)) with
+// u = sqrt(2/pi) (x + 0.044715 x^3), evaluated through the identity
+// 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)). Saturates correctly at both
+// ends: exp overflow gives x / inf = -0 for large negative x.
+__device__ __forceinline__ float gelu_tanh(float x)
+{
+  const float u = 0.7978845608028654f * fmaf(0.044715f * x, x * x, x);
+  return x / (1.0f + __expf(-2.0f * u));
+}
+
+// ---- internal launcher interface ------------------------------------------
+
+// Element type of a bias vector (matches LTX25_DT_* in the C header).
+enum BiasType : int { kBiasNone = 0, kBiasBf16 = 1, kBiasF32 = 2 };
+enum Epilogue : int { kEpiNone = 0, kEpiGelu = 1 };
+
+// One GEMM y[M][N] = x[M][K] . W[N][K]^T with W either group-affine codes
+// (bits 8 or 4, `group` 32 or 64) or dense bf16 (bits 16).
+struct GemmDesc {
+  const uint16_t* x = nullptr;
+  const void* w = nullptr;          // u8/u32 codes, or bf16 dense
+  const uint16_t* scales = nullptr;
+  const uint16_t* qbias = nullptr;
+  int bits = 8;                     // 8, 4, or 16 (= dense bf16)
+  int group = 64;
+  const void* bias = nullptr;
+  int bias_type = kBiasNone;
+  int epilogue = kEpiNone;
+  uint16_t* y = nullptr;
+  int M = 0, N = 0, K = 0;
+};
+
+// The tile configuration a GEMM runs with, chosen on the host.
+struct GemmPlan {
+  int tile = 0;      // 0 = 256x256 (tall), 1 = 128x128 (skinny / mid)
+  int splits = 1;    // split-K factor
+  int k_chunk = 0;   // K elements per split (multiple of 64)
+  size_t workspace_bytes = 0;   // f32 partials when splits > 1
+};
+
+GemmPlan plan_gemm(int M, int N, int K, int cu_count);
+hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
+                       float* workspace, hipStream_t stream);
+
+hipError_t launch_bias_add(uint16_t* y, const void* bias, int bias_type,
+                           int M, int N, hipStream_t stream);
+hipError_t launch_gelu(const uint16_t* x, uint16_t* y, size_t n,
+                       hipStream_t stream);
+hipError_t launch_dequant(const void* codes, const uint16_t* scales,
+                          const uint16_t* qbias, int bits, int group,
+                          uint16_t* out, int N, int K, hipStream_t stream);
+hipError_t launch_quantize_affine(const float* w, uint32_t* codes,
+                                  uint16_t* scales, uint16_t* qbias, int N,
+                                  int K, int bits, int group,
+                                  hipStream_t stream);
+hipError_t launch_pack(const uint8_t* q, uint32_t* codes, int N, int K,
+                       int bits, hipStream_t stream);
+hipError_t launch_unpack(const uint32_t* codes, uint8_t* q, int N, int K,
+                         int bits, hipStream_t stream);
+hipError_t launch_f16_to_bf16(const uint16_t* in, uint16_t* out, size_t n,
+                              hipStream_t stream);
+
+hipError_t launch_i8_quantize_rows(const uint16_t* x, int8_t* q, float* s,
+                                   int M, int K, hipStream_t stream);
+hipError_t launch_i8_quantize_qweight(const void* codes,
+                                      const uint16_t* scales,
+                                      const uint16_t* qbias, int bits,
+                                      int group, int8_t* q, float* s, int N,
+                                      int K, hipStream_t stream);
+hipError_t launch_i8_gemm(const int8_t* xq, const float* sx,
+                          const int8_t* wq, const float* sw, const void* bias,
+                          int bias_type, uint16_t* y, int32_t* acc, int M,
+                          int K, int N, hipStream_t stream);
+
+}  // namespace ltx25

@@ -1,0 +1,291 @@
+// Bandwidth-bound kernels around the quantized linear: the standalone bias
+// pass, GELU-tanh, the dequant-once expansion, the packed-weight format
+// (pack / unpack / quantize) and the loader's F16 -> bf16 conversion.
+// All are HBM-bound byte work: 16-byte vector loads and stores, no LDS.
+#include "common.h"
+
+namespace ltx25 {
+namespace {
+
+constexpr int kBlock = 256;
+
+unsigned blocks_for(size_t work_items)
+{
+  return (unsigned)((work_items + kBlock - 1) / kBlock);
+}
+
+// y = bf16(f32(y) + f32(bias[i % N])), 8 elements per thread.
+// Semantics of ltx_bias_add (src/ltx25-kernels.metal:1431-1441).
+__global__ void __launch_bounds__(kBlock)
+bias_add_kernel(uint16_t* y, const void* bias, int bias_type, int N,
+                size_t total)
+{
+  const size_t i0 = ((size_t)blockIdx.x * kBlock + threadIdx.x) * 8;
+  if (i0 >= total) { return; }
+  auto bias_at = [&](size_t i) -> float {
+    const int n = (int)(i % (size_t)N);
+    return bias_type == kBiasF32 ? ((const float*)bias)[n]
+                                 : bf16_to_f32(((const uint16_t*)bias)[n]);
+  };
+  if (i0 + 8 <= total && (N & 7) == 0) {
+    uint4 v = *(const uint4*)(y + i0);
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = bf16_to_f32((uint16_t)(w[j] & 0xffffu)) + bias_at(i0 + 2 * j);
+      const float b = bf16_to_f32((uint16_t)(w[j] >> 16)) + bias_at(i0 + 2 * j + 1);
+      w[j] = pack_bf16x2(a, b);
+    }
+    *(uint4*)(y + i0) = make_uint4(w[0], w[1], w[2], w[3]);
+    return;
+  }
+  for (size_t i = i0; i < i0 + 8 && i < total; ++i) {
+    y[i] = f32_to_bf16(bf16_to_f32(y[i]) + bias_at(i));
+  }
+}
+
+__global__ void __launch_bounds__(kBlock)
+gelu_kernel(const uint16_t* x, uint16_t* y, size_t n)
+{
+  const size_t i0 = ((size_t)blockIdx.x * kBlock + threadIdx.x) * 8;
+  if (i0 >= n) { return; }
+  if (i0 + 8 <= n) {
+    const uint4 v = *(const uint4*)(x + i0);
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      w[j] = pack_bf16x2(gelu_tanh(bf16_to_f32((uint16_t)(w[j] & 0xffffu))),
+                         gelu_tanh(bf16_to_f32((uint16_t)(w[j] >> 16))));
+    }
+    *(uint4*)(y + i0) = make_uint4(w[0], w[1], w[2], w[3]);
+    return;
+  }
+  for (size_t i = i0; i < n; ++i) {
+    y[i] = f32_to_bf16(gelu_tanh(bf16_to_f32(x[i])));
+  }
+}
+
+// Dequant-once: 16 codes (w8) or 32 codes (w4) per thread, one 16-byte
+// load, w = bf16(fma(scale, q, qbias)) stored as 2 or 4 16-byte stores.
+template <int BITS>
+__global__ void __launch_bounds__(kBlock)
+dequant_kernel(const uint8_t* codes, const uint16_t* scales,
+               const uint16_t* qbias, int gshift, int gcols, uint16_t* out,
+               int N, int K)
+{
+  constexpr int CPC = 128 / BITS;          // codes per 16-byte chunk
+  const int chunks_per_row = K / CPC;
+  const size_t c = (size_t)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= (size_t)N * chunks_per_row) { return; }
+  const int n = (int)(c / chunks_per_row);
+  const int k0 = (int)(c % chunks_per_row) * CPC;
+  const uint4 v = *(const uint4*)(codes + (size_t)n * K * BITS / 8 + (size_t)k0 * BITS / 8);
+  const size_t gi = (size_t)n * gcols + (k0 >> gshift);
+  const float s = bf16_to_f32(scales[gi]);
+  const float b = bf16_to_f32(qbias[gi]);
+  const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+  uint16_t* dst = out + (size_t)n * K + k0;
+  if constexpr (BITS == 8) {
+    uint32_t o[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[2 * j] = pack_bf16x2(fmaf(s, (float)(wv[j] & 0xffu), b),
+                             fmaf(s, (float)((wv[j] >> 8) & 0xffu), b));
+      o[2 * j + 1] = pack_bf16x2(fmaf(s, (float)((wv[j] >> 16) & 0xffu), b),
+                                 fmaf(s, (float)(wv[j] >> 24), b));
+    }
+    *(uint4*)dst = make_uint4(o[0], o[1], o[2], o[3]);
+    *(uint4*)(dst + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+  } else {
+    uint32_t o[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t q0 = (wv[j] >> (8 * t)) & 0xfu;
+        const uint32_t q1 = (wv[j] >> (8 * t + 4)) & 0xfu;
+        o[4 * j + t] = pack_bf16x2(fmaf(s, (float)q0, b), fmaf(s, (float)q1, b));
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      *(uint4*)(dst + 8 * t) = make_uint4(o[4 * t], o[4 * t + 1], o[4 * t + 2], o[4 * t + 3]);
+    }
+  }
+}
+
+// Group-affine quantize, one thread per (row, group). Step for step the
+// quantizer of tests/ltx25-qlinear-test.cc:108-139: fmin/fmax over the
+// group, scale and min rounded to bf16 first, codes by round-half-away of
+// (w - bias) / scale with IEEE division, clamped; LOW bits first.
+__global__ void __launch_bounds__(kBlock)
+quantize_affine_kernel(const float* w, uint32_t* codes, uint16_t* scales,
+                       uint16_t* qbias, int N, int K, int bits, int group)
+{
+  const int gcols = K / group;
+  const size_t gid = (size_t)blockIdx.x * kBlock + threadIdx.x;
+  if (gid >= (size_t)N * gcols) { return; }
+  const int n = (int)(gid / gcols);
+  const int g = (int)(gid % gcols);
+  const float* wr = w + (size_t)n * K + (size_t)g * group;
+  float lo = wr[0], hi = wr[0];
+  for (int j = 1; j < group; ++j) {
+    lo = fminf(lo, wr[j]);
+    hi = fmaxf(hi, wr[j]);
+  }
+  const float qmax = (float)((1 << bits) - 1);
+  const uint16_t sc_b = f32_to_bf16((hi - lo) / qmax);
+  const uint16_t lo_b = f32_to_bf16(lo);
+  scales[gid] = sc_b;
+  qbias[gid] = lo_b;
+  const float scr = bf16_to_f32(sc_b);
+  const float lor = bf16_to_f32(lo_b);
+  const int per_word = 32 / bits;
+  uint32_t* dst = codes + ((size_t)n * K + (size_t)g * group) / per_word;
+  for (int wd = 0; wd < group / per_word; ++wd) {
+    uint32_t word = 0;
+    for (int s = 0; s < per_word; ++s) {
+      const float v = wr[wd * per_word + s];
+      float q = scr > 0.0f ? roundf((v - lor) / scr) : 0.0f;
+      q = fminf(fmaxf(q, 0.0f), qmax);
+      word |= (uint32_t)q << (bits * s);
+    }
+    dst[wd] = word;
+  }
+}
+
+// u8 codes [N][K] <-> u32 words, LOW bits first; one word per thread.
+__global__ void __launch_bounds__(kBlock)
+pack_kernel(const uint8_t* q, uint32_t* codes, size_t words, int bits)
+{
+  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= words) { return; }
+  const int per_word = 32 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  uint32_t v = 0;
+  for (int s = 0; s < per_word; ++s) {
+    v |= ((uint32_t)q[i * per_word + s] & mask) << (bits * s);
+  }
+  codes[i] = v;
+}
+
+__global__ void __launch_bounds__(kBlock)
+unpack_kernel(const uint32_t* codes, uint8_t* q, size_t words, int bits)
+{
+  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= words) { return; }
+  const int per_word = 32 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  const uint32_t v = codes[i];
+  for (int s = 0; s < per_word; ++s) {
+    q[i * per_word + s] = (uint8_t)((v >> (bits * s)) & mask);
+  }
+}
+
+// F16 -> f32 (exact) -> bf16 (RNE), 8 per thread; in place allowed.
+__global__ void __launch_bounds__(kBlock)
+f16_to_bf16_kernel(const uint16_t* in, uint16_t* out, size_t n)
+{
+  const size_t i0 = ((size_t)blockIdx.x * kBlock + threadIdx.x) * 8;
+  if (i0 >= n) { return; }
+  auto cvt = [](uint16_t h) -> float {
+    return (float)__builtin_bit_cast(_Float16, h);
+  };
+  if (i0 + 8 <= n) {
+    const uint4 v = *(const uint4*)(in + i0);
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      w[j] = pack_bf16x2(cvt((uint16_t)(w[j] & 0xffffu)), cvt((uint16_t)(w[j] >> 16)));
+    }
+    *(uint4*)(out + i0) = make_uint4(w[0], w[1], w[2], w[3]);
+    return;
+  }
+  for (size_t i = i0; i < n; ++i) { out[i] = f32_to_bf16(cvt(in[i])); }
+}
+
+int ilog2(int v)
+{
+  int s = 0;
+  while ((1 << s) < v) { ++s; }
+  return s;
+}
+
+}  // namespace
+
+hipError_t launch_bias_add(uint16_t* y, const void* bias, int bias_type,
+                           int M, int N, hipStream_t stream)
+{
+  const size_t total = (size_t)M * N;
+  hipLaunchKernelGGL(bias_add_kernel, dim3(blocks_for((total + 7) / 8)),
+                     dim3(kBlock), 0, stream, y, bias, bias_type, N, total);
+  return hipGetLastError();
+}
+
+hipError_t launch_gelu(const uint16_t* x, uint16_t* y, size_t n,
+                       hipStream_t stream)
+{
+  hipLaunchKernelGGL(gelu_kernel, dim3(blocks_for((n + 7) / 8)), dim3(kBlock),
+                     0, stream, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant(const void* codes, const uint16_t* scales,
+                          const uint16_t* qbias, int bits, int group,
+                          uint16_t* out, int N, int K, hipStream_t stream)
+{
+  const int cpc = 128 / bits;
+  const size_t chunks = (size_t)N * (K / cpc);
+  const int gshift = ilog2(group);
+  const int gcols = K / group;
+  if (bits == 8) {
+    hipLaunchKernelGGL(dequant_kernel<8>, dim3(blocks_for(chunks)),
+                       dim3(kBlock), 0, stream, (const uint8_t*)codes, scales,
+                       qbias, gshift, gcols, out, N, K);
+  } else {
+    hipLaunchKernelGGL(dequant_kernel<4>, dim3(blocks_for(chunks)),
+                       dim3(kBlock), 0, stream, (const uint8_t*)codes, scales,
+                       qbias, gshift, gcols, out, N, K);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_affine(const float* w, uint32_t* codes,
+                                  uint16_t* scales, uint16_t* qbias, int N,
+                                  int K, int bits, int group,
+                                  hipStream_t stream)
+{
+  const size_t groups = (size_t)N * (K / group);
+  hipLaunchKernelGGL(quantize_affine_kernel, dim3(blocks_for(groups)),
+                     dim3(kBlock), 0, stream, w, codes, scales, qbias, N, K,
+                     bits, group);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack(const uint8_t* q, uint32_t* codes, int N, int K,
+                       int bits, hipStream_t stream)
+{
+  const size_t words = (size_t)N * K * bits / 32;
+  hipLaunchKernelGGL(pack_kernel, dim3(blocks_for(words)), dim3(kBlock), 0,
+                     stream, q, codes, words, bits);
+  return hipGetLastError();
+}
+
+hipError_t launch_unpack(const uint32_t* codes, uint8_t* q, int N, int K,
+                         int bits, hipStream_t stream)
+{
+  const size_t words = (size_t)N * K * bits / 32;
+  hipLaunchKernelGGL(unpack_kernel, dim3(blocks_for(words)), dim3(kBlock), 0,
+                     stream, codes, q, words, bits);
+  return hipGetLastError();
+}
+
+hipError_t launch_f16_to_bf16(const uint16_t* in, uint16_t* out, size_t n,
+                              hipStream_t stream)
+{
+  hipLaunchKernelGGL(f16_to_bf16_kernel, dim3(blocks_for((n + 7) / 8)),
+                     dim3(kBlock), 0, stream, in, out, n);
+  return hipGetLastError();
+}
+
+}  // namespace ltx25

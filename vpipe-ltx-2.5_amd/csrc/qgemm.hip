@@ -1,0 +1,420 @@
+// The quantized linear on gfx950: y = x . dequant(W)^T (+ bias) (+ GELU).
+//
+// One kernel template serves every weight format (w8 / w4 group-affine
+// codes, or dense bf16) and both tile shapes:
+//
+//   tall   BM x BN = 256 x 256, 4 waves in 2 x 2, 128 x 128 per wave
+//          (the video GEMMs, thousands of tokens)
+//   skinny BM x BN = 128 x 128, 4 waves in 2 x 2, 64 x 64 per wave,
+//          with split-K across workgroups (the audio GEMMs at ~126 tokens
+//          and anything else too small to fill 256 CUs)
+//
+// Per K step of 64 (one w8g64 group):
+//   - X rows stream from HBM as 16-byte loads into registers, then to LDS;
+//   - weight codes stream as 16-byte loads (16 u8 codes or 32 u4 codes),
+//     are dequantized ONCE per workgroup in registers,
+//     w = bf16(fma(scale, q, qbias)), and land in LDS as bf16;
+//   - each wave reads 32x16 bf16 fragments from LDS and issues
+//     v_mfma_f32_32x32x16_bf16 with f32 accumulation.
+// The next step's global loads are issued before the current step's MFMAs
+// and land in the other LDS stage afterwards (two stages, one barrier per
+// step). The bias add (f32 or bf16) and GELU-tanh are fused into the
+// epilogue, ahead of the single rounding to bf16; with split-K the
+// epilogue runs in a reduction kernel that sums the f32 partials in a
+// fixed order, so results are deterministic.
+//
+// Reference semantics: MetalOps::linear(QWeight) (src/ltx25-metal-ops.cc:
+// 531-569) computes the same product through affine_dequant + dense_gemm_mma
+// (or affine_qmm_steel), then a separate ltx_bias_add pass.
+#include "common.h"
+
+#include <algorithm>
+
+namespace ltx25 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kBK = 64;             // K per main-loop step
+constexpr int kLdsRow = kBK + 8;    // bf16 per LDS row: 144 B pitch keeps
+                                    // the 16 B fragment reads conflict-free
+
+struct KParams {
+  const uint16_t* x;
+  const uint8_t* wq;       // codes as bytes (bits 8 or 4)
+  const uint16_t* wd;      // dense bf16 weight (bits 16)
+  const uint16_t* scales;
+  const uint16_t* qbias;
+  const void* bias;
+  uint16_t* y;
+  float* partial;          // [splits][M][N] when split
+  int M, N, K;
+  int gshift;              // log2(group)
+  int gcols;               // K / group
+  int k_chunk;
+  int bias_type;
+  int epilogue;
+  int tiles_m, tiles_n;
+};
+
+// Workgroup id -> (tile_m, tile_n). Consecutive workgroup ids are dealt
+// round-robin to the 8 XCDs, so the id is first remapped so that each XCD
+// receives a contiguous range of tiles, then the range is walked in groups
+// of 8 M-tiles: the workgroups an XCD runs at once share X and W tiles in
+// that XCD's L2.
+__device__ __forceinline__ void map_tile(int bid, int tiles_m, int tiles_n,
+                                         int& tm, int& tn)
+{
+  const int total = tiles_m * tiles_n;
+  const int total8 = total & ~7;
+  int pid = bid;
+  if (bid < total8) { pid = (bid & 7) * (total8 >> 3) + (bid >> 3); }
+  constexpr int kGroupM = 8;
+  const int per_group = kGroupM * tiles_n;
+  const int gid = pid / per_group;
+  const int first_m = gid * kGroupM;
+  const int gsz = min(tiles_m - first_m, kGroupM);
+  const int r = pid - gid * per_group;
+  tm = first_m + r % gsz;
+  tn = r / gsz;
+}
+
+__device__ __forceinline__ float load_bias(const void* bias, int type, int n)
+{
+  if (type == kBiasBf16) { return bf16_to_f32(((const uint16_t*)bias)[n]); }
+  if (type == kBiasF32) { return ((const float*)bias)[n]; }
+  return 0.0f;
+}
+
+template <int BM, int BN, int WM, int WN, int BITS, bool SPLIT>
+__global__ void __launch_bounds__(kThreads)
+qgemm_kernel(KParams p)
+{
+  constexpr int WTM = BM / WM;
+  constexpr int WTN = BN / WN;
+  constexpr int FM = WTM / 32;
+  constexpr int FN = WTN / 32;
+  constexpr int A_LD = BM * 8 / kThreads;            // 16 B chunks / thread
+  constexpr int B_CPR = BITS == 16 ? 8 : kBK * BITS / 8 / 16;  // chunks/row
+  constexpr int B_LD = BN * B_CPR / kThreads;
+  constexpr int B_RSTEP = kThreads / B_CPR;
+  constexpr int CPC = BITS == 16 ? 8 : 128 / BITS;   // codes per chunk
+  static_assert(A_LD >= 1 && B_LD >= 1, "tile too small for 256 threads");
+
+  __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][BN * kLdsRow];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+
+  int tm, tn;
+  map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+  const int split = SPLIT ? (int)blockIdx.y : 0;
+  const int kbeg = split * p.k_chunk;
+  const int kend = min(p.K, kbeg + p.k_chunk);
+  const int nsteps = kend > kbeg ? (kend - kbeg) / kBK : 0;
+
+  const int a_c = tid & 7;
+  const int a_r = tid >> 3;
+  const int b_c = tid % B_CPR;
+  const int b_r = tid / B_CPR;
+
+  uint4 areg[A_LD];
+  uint4 breg[B_LD];
+  float bsc[B_LD];
+  float bbi[B_LD];
+
+  const size_t wrow_bytes = (size_t)p.K * (BITS == 16 ? 2 : BITS) / 8;
+
+  auto load_tiles = [&](int k) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int m = m0 + a_r + 32 * i;
+      areg[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (m < p.M) {
+        areg[i] = *(const uint4*)(p.x + (size_t)m * p.K + k + a_c * 8);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int n = n0 + b_r + B_RSTEP * i;
+      breg[i] = make_uint4(0u, 0u, 0u, 0u);
+      bsc[i] = 0.0f;
+      bbi[i] = 0.0f;
+      if (n < p.N) {
+        if constexpr (BITS == 16) {
+          breg[i] = *(const uint4*)(p.wd + (size_t)n * p.K + k + b_c * 8);
+        } else {
+          breg[i] = *(const uint4*)(p.wq + (size_t)n * wrow_bytes +
+                                    (size_t)k * BITS / 8 + b_c * 16);
+          const size_t gi = (size_t)n * p.gcols + ((k + b_c * CPC) >> p.gshift);
+          bsc[i] = bf16_to_f32(p.scales[gi]);
+          bbi[i] = bf16_to_f32(p.qbias[gi]);
+        }
+      }
+    }
+  };
+
+  auto store_tiles = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      *(uint4*)&lds_a[st][(a_r + 32 * i) * kLdsRow + a_c * 8] = areg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      uint16_t* dst = &lds_b[st][(b_r + B_RSTEP * i) * kLdsRow + b_c * CPC];
+      if constexpr (BITS == 16) {
+        *(uint4*)dst = breg[i];
+      } else if constexpr (BITS == 8) {
+        const uint32_t wv[4] = {breg[i].x, breg[i].y, breg[i].z, breg[i].w};
+        const float s = bsc[i], b = bbi[i];
+        uint32_t o[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t v = wv[j];
+          o[2 * j] = pack_bf16x2(fmaf(s, (float)(v & 0xffu), b),
+                                 fmaf(s, (float)((v >> 8) & 0xffu), b));
+          o[2 * j + 1] = pack_bf16x2(fmaf(s, (float)((v >> 16) & 0xffu), b),
+                                     fmaf(s, (float)(v >> 24), b));
+        }
+        *(uint4*)dst = make_uint4(o[0], o[1], o[2], o[3]);
+        *(uint4*)(dst + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+      } else {
+        // w4: code 8j+s sits at bits 4s of word j. Even codes are the low
+        // nibbles of each byte, odd codes the high nibbles.
+        const uint32_t wv[4] = {breg[i].x, breg[i].y, breg[i].z, breg[i].w};
+        const float s = bsc[i], b = bbi[i];
+        uint32_t o[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t lo = wv[j] & 0x0f0f0f0fu;
+          const uint32_t hi = (wv[j] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            o[4 * j + t] =
+                pack_bf16x2(fmaf(s, (float)((lo >> (8 * t)) & 0xffu), b),
+                            fmaf(s, (float)((hi >> (8 * t)) & 0xffu), b));
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          *(uint4*)(dst + 8 * t) =
+              make_uint4(o[4 * t], o[4 * t + 1], o[4 * t + 2], o[4 * t + 3]);
+        }
+      }
+    }
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { acc[i][j][r] = 0.0f; }
+    }
+  }
+
+  if (nsteps > 0) {
+    load_tiles(kbeg);
+    store_tiles(0);
+    __syncthreads();
+    for (int s = 0; s < nsteps; ++s) {
+      const int st = s & 1;
+      const bool more = s + 1 < nsteps;
+      if (more) { load_tiles(kbeg + (s + 1) * kBK); }
+      const uint16_t* la = lds_a[st] + (wm * WTM + (lane & 31)) * kLdsRow +
+                           (lane >> 5) * 8;
+      const uint16_t* lb = lds_b[st] + (wn * WTN + (lane & 31)) * kLdsRow +
+                           (lane >> 5) * 8;
+#pragma unroll
+      for (int kk = 0; kk < kBK / 16; ++kk) {
+        bf16x8 af[FM];
+        bf16x8 bfv[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          af[i] = *(const bf16x8*)(la + i * 32 * kLdsRow + kk * 16);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          bfv[j] = *(const bf16x8*)(lb + j * 32 * kLdsRow + kk * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                af[i], bfv[j], acc[i][j], 0, 0, 0);
+          }
+        }
+      }
+      if (more) { store_tiles(st ^ 1); }
+      __syncthreads();
+    }
+  }
+
+  // Accumulator layout of the 32x32 f32 MFMA result: lane l, register r
+  // holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = n0 + wn * WTN + j * 32 + (lane & 31);
+    float bv = 0.0f;
+    if (!SPLIT && n < p.N) { bv = load_bias(p.bias, p.bias_type, n); }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int mb = m0 + wm * WTM + i * 32 + (lane >> 5) * 4;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = mb + (r >> 2) * 8 + (r & 3);
+        if (m < p.M && n < p.N) {
+          float v = acc[i][j][r];
+          if constexpr (SPLIT) {
+            p.partial[((size_t)split * p.M + m) * p.N + n] = v;
+          } else {
+            v += bv;
+            if (p.epilogue == kEpiGelu) { v = gelu_tanh(v); }
+            p.y[(size_t)m * p.N + n] = f32_to_bf16(v);
+          }
+        }
+      }
+    }
+  }
+}
+
+// Sum the split-K partials in split order, then bias, epilogue, bf16.
+__global__ void __launch_bounds__(256)
+splitk_reduce_kernel(const float* partial, int splits, const void* bias,
+                     int bias_type, int epilogue, uint16_t* y, int M, int N)
+{
+  const size_t total = (size_t)M * N;
+  const size_t i0 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i0 >= total) { return; }
+  const size_t plane = total;
+  if ((N & 3) == 0 && i0 + 4 <= total) {
+    f32x4 s = *(const f32x4*)(partial + i0);
+    for (int k = 1; k < splits; ++k) {
+      const f32x4 v = *(const f32x4*)(partial + (size_t)k * plane + i0);
+      s += v;
+    }
+    const int n = (int)(i0 % (size_t)N);
+    float o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float v = s[t] + load_bias(bias, bias_type, n + t);
+      if (epilogue == kEpiGelu) { v = gelu_tanh(v); }
+      o[t] = v;
+    }
+    uint2 packed = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+    *(uint2*)(y + i0) = packed;
+    return;
+  }
+  for (size_t i = i0; i < i0 + 4 && i < total; ++i) {
+    float v = partial[i];
+    for (int k = 1; k < splits; ++k) { v += partial[(size_t)k * plane + i]; }
+    v += load_bias(bias, bias_type, (int)(i % (size_t)N));
+    if (epilogue == kEpiGelu) { v = gelu_tanh(v); }
+    y[i] = f32_to_bf16(v);
+  }
+}
+
+template <int BM, int BN, int BITS, bool SPLIT>
+hipError_t launch_cfg(const KParams& kp, int splits, hipStream_t stream)
+{
+  const dim3 grid((unsigned)(kp.tiles_m * kp.tiles_n), (unsigned)splits, 1);
+  hipLaunchKernelGGL((qgemm_kernel<BM, BN, 2, 2, BITS, SPLIT>), grid,
+                     dim3(kThreads), 0, stream, kp);
+  return hipGetLastError();
+}
+
+template <int BM, int BN>
+hipError_t launch_tile(const KParams& kp, int bits, int splits,
+                       hipStream_t stream)
+{
+  const bool split = splits > 1;
+  switch (bits) {
+    case 8:
+      return split ? launch_cfg<BM, BN, 8, true>(kp, splits, stream)
+                   : launch_cfg<BM, BN, 8, false>(kp, splits, stream);
+    case 4:
+      return split ? launch_cfg<BM, BN, 4, true>(kp, splits, stream)
+                   : launch_cfg<BM, BN, 4, false>(kp, splits, stream);
+    default:
+      return split ? launch_cfg<BM, BN, 16, true>(kp, splits, stream)
+                   : launch_cfg<BM, BN, 16, false>(kp, splits, stream);
+  }
+}
+
+int ilog2(int v)
+{
+  int s = 0;
+  while ((1 << s) < v) { ++s; }
+  return s;
+}
+
+}  // namespace
+
+GemmPlan plan_gemm(int M, int N, int K, int cu_count)
+{
+  GemmPlan plan;
+  const long tall_tiles = (long)((M + 255) / 256) * ((N + 255) / 256);
+  if (M > 128 && tall_tiles >= cu_count) {
+    plan.tile = 0;
+    plan.splits = 1;
+    plan.k_chunk = K;
+    return plan;
+  }
+  plan.tile = 1;
+  const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
+  const long want = (2L * cu_count + tiles - 1) / tiles;
+  const int max_split = std::max(1, K / 256);
+  int s = (int)std::min<long>(std::max<long>(want, 1), max_split);
+  int chunk = ((K + s - 1) / s + kBK - 1) / kBK * kBK;
+  s = (K + chunk - 1) / chunk;
+  plan.splits = s;
+  plan.k_chunk = chunk;
+  plan.workspace_bytes = s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
+  return plan;
+}
+
+hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
+                       float* workspace, hipStream_t stream)
+{
+  KParams kp;
+  kp.x = d.x;
+  kp.wq = (const uint8_t*)d.w;
+  kp.wd = (const uint16_t*)d.w;
+  kp.scales = d.scales;
+  kp.qbias = d.qbias;
+  kp.bias = d.bias;
+  kp.y = d.y;
+  kp.partial = workspace;
+  kp.M = d.M;
+  kp.N = d.N;
+  kp.K = d.K;
+  kp.gshift = d.bits == 16 ? 0 : ilog2(d.group);
+  kp.gcols = d.bits == 16 ? 0 : d.K / d.group;
+  kp.k_chunk = plan.k_chunk;
+  kp.bias_type = d.bias != nullptr ? d.bias_type : kBiasNone;
+  kp.epilogue = d.epilogue;
+  const int bm = plan.tile == 0 ? 256 : 128;
+  const int bn = plan.tile == 0 ? 256 : 128;
+  kp.tiles_m = (d.M + bm - 1) / bm;
+  kp.tiles_n = (d.N + bn - 1) / bn;
+
+  hipError_t e = plan.tile == 0
+                     ? launch_tile<256, 256>(kp, d.bits, plan.splits, stream)
+                     : launch_tile<128, 128>(kp, d.bits, plan.splits, stream);
+  if (e != hipSuccess || plan.splits <= 1) { return e; }
+  const size_t total = (size_t)d.M * d.N;
+  const unsigned blocks = (unsigned)((total + 1023) / 1024);
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream,
+                     (const float*)workspace, plan.splits, kp.bias,
+                     kp.bias_type, d.epilogue, d.y, d.M, d.N);
+  return hipGetLastError();
+}
+
+}  // namespace ltx25
