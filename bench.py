@@ -370,6 +370,9 @@ def main():
     ap.add_argument("--skip-audio", action="store_true")
     ap.add_argument("--skip-i8", action="store_true")
     ap.add_argument("--skip-c4", action="store_true")
+    ap.add_argument("--profile-copy", action="store_true",
+                    help="also run one plain 256 MiB device copy, the known-size kernel that "
+                         "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -405,6 +408,13 @@ def main():
         extra["c4"] = bench_c4(pkg, torch, steps=2, warmup=1)
         log(f"  {extra['c4']['s_per_denoise_step']:.3f} s/step")
         torch.cuda.empty_cache()
+    if args.profile_copy:
+        src = torch.ones((256 << 20,), dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     cpu = None
     if not args.skip_cpu:
         log("CPU baseline")

@@ -29,6 +29,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace ltx25 {
 namespace {
@@ -85,6 +86,28 @@ __device__ __forceinline__ float load_bias(const void* bias, int type, int n)
   return 0.0f;
 }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p,
+                                                           size_t bytes)
+{
+  // Raw buffer resource: loads at offsets past `bytes` return zeros, which
+  // is how rows past M and N are handled without branches.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
+                                           (int)(uint32_t)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r,
+                                            uint32_t voff, uint32_t soff)
+{
+  const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+
+__device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r,
+                                              uint32_t voff, uint32_t soff)
+{
+  return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+}
+
 template <int BM, int BN, int WM, int WN, int BITS, bool SPLIT>
 __global__ void __launch_bounds__(kThreads)
 qgemm_kernel(KParams p)
@@ -98,6 +121,7 @@ qgemm_kernel(KParams p)
   constexpr int B_LD = BN * B_CPR / kThreads;
   constexpr int B_RSTEP = kThreads / B_CPR;
   constexpr int CPC = BITS == 16 ? 8 : 128 / BITS;   // codes per chunk
+  constexpr bool QUANT = BITS != 16;
   static_assert(A_LD >= 1 && B_LD >= 1, "tile too small for 256 threads");
 
   __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * kLdsRow];
@@ -123,55 +147,71 @@ qgemm_kernel(KParams p)
   const int b_c = tid % B_CPR;
   const int b_r = tid / B_CPR;
 
+  // Buffer resources and per-thread byte offsets, fixed for the whole loop;
+  // each step adds a uniform K offset (an SGPR).
+  const size_t wrow_bytes = (size_t)p.K * (QUANT ? BITS : 16) / 8;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, (size_t)p.M * p.K * 2);
+  const __amdgpu_buffer_rsrc_t wr =
+      make_rsrc(QUANT ? (const void*)p.wq : (const void*)p.wd, (size_t)p.N * wrow_bytes);
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(p.scales, (size_t)p.N * p.gcols * 2);
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(p.qbias, (size_t)p.N * p.gcols * 2);
+  uint32_t a_off[A_LD];
+  uint32_t b_off[B_LD];
+  uint32_t s_off[B_LD];
+#pragma unroll
+  for (int i = 0; i < A_LD; ++i) {
+    a_off[i] = (uint32_t)(((size_t)(m0 + a_r + 32 * i) * p.K + a_c * 8) * 2);
+  }
+#pragma unroll
+  for (int i = 0; i < B_LD; ++i) {
+    const size_t n = (size_t)(n0 + b_r + B_RSTEP * i);
+    b_off[i] = (uint32_t)(n * wrow_bytes + b_c * 16);
+    s_off[i] = QUANT ? (uint32_t)((n * p.gcols + ((b_c * CPC) >> p.gshift)) * 2) : 0u;
+  }
+
   uint4 areg[A_LD];
   uint4 breg[B_LD];
-  float bsc[B_LD];
-  float bbi[B_LD];
+  uint16_t sraw[B_LD];
+  uint16_t qraw[B_LD];
 
-  const size_t wrow_bytes = (size_t)p.K * (BITS == 16 ? 2 : BITS) / 8;
-
-  auto load_tiles = [&](int k) {
+  auto load_a = [&](int k) {
 #pragma unroll
-    for (int i = 0; i < A_LD; ++i) {
-      const int m = m0 + a_r + 32 * i;
-      areg[i] = make_uint4(0u, 0u, 0u, 0u);
-      if (m < p.M) {
-        areg[i] = *(const uint4*)(p.x + (size_t)m * p.K + k + a_c * 8);
-      }
-    }
+    for (int i = 0; i < A_LD; ++i) { areg[i] = buf_load16(xr, a_off[i], (uint32_t)k * 2); }
+  };
+  auto load_b = [&](int k) {
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
-      const int n = n0 + b_r + B_RSTEP * i;
-      breg[i] = make_uint4(0u, 0u, 0u, 0u);
-      bsc[i] = 0.0f;
-      bbi[i] = 0.0f;
-      if (n < p.N) {
-        if constexpr (BITS == 16) {
-          breg[i] = *(const uint4*)(p.wd + (size_t)n * p.K + k + b_c * 8);
-        } else {
-          breg[i] = *(const uint4*)(p.wq + (size_t)n * wrow_bytes +
-                                    (size_t)k * BITS / 8 + b_c * 16);
-          const size_t gi = (size_t)n * p.gcols + ((k + b_c * CPC) >> p.gshift);
-          bsc[i] = bf16_to_f32(p.scales[gi]);
-          bbi[i] = bf16_to_f32(p.qbias[gi]);
-        }
+      breg[i] = buf_load16(wr, b_off[i], (uint32_t)k * (QUANT ? BITS : 16) / 8);
+      if constexpr (QUANT) {
+        const uint32_t so = (uint32_t)(k >> p.gshift) * 2;
+        sraw[i] = buf_load2(sr, s_off[i], so);
+        qraw[i] = buf_load2(qr, s_off[i], so);
       }
     }
   };
+  auto load_regs = [&](int k) {
+    load_a(k);
+    load_b(k);
+  };
 
-  auto store_tiles = [&](int st) {
+  auto store_a = [&](int st) {
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
       *(uint4*)&lds_a[st][(a_r + 32 * i) * kLdsRow + a_c * 8] = areg[i];
     }
+  };
+
+  // Weight rows [lo, hi) of this thread's B_LD chunks: dequantize (for
+  // codes) and write to LDS stage `st`.
+  auto store_b_rows = [&](int st, int lo, int hi) {
 #pragma unroll
-    for (int i = 0; i < B_LD; ++i) {
+    for (int i = lo; i < hi; ++i) {
       uint16_t* dst = &lds_b[st][(b_r + B_RSTEP * i) * kLdsRow + b_c * CPC];
-      if constexpr (BITS == 16) {
+      if constexpr (!QUANT) {
         *(uint4*)dst = breg[i];
       } else if constexpr (BITS == 8) {
         const uint32_t wv[4] = {breg[i].x, breg[i].y, breg[i].z, breg[i].w};
-        const float s = bsc[i], b = bbi[i];
+        const float s = bf16_to_f32(sraw[i]), b = bf16_to_f32(qraw[i]);
         uint32_t o[8];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -187,7 +227,7 @@ qgemm_kernel(KParams p)
         // w4: code 8j+s sits at bits 4s of word j. Even codes are the low
         // nibbles of each byte, odd codes the high nibbles.
         const uint32_t wv[4] = {breg[i].x, breg[i].y, breg[i].z, breg[i].w};
-        const float s = bsc[i], b = bbi[i];
+        const float s = bf16_to_f32(sraw[i]), b = bf16_to_f32(qraw[i]);
         uint32_t o[16];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -209,6 +249,8 @@ qgemm_kernel(KParams p)
     }
   };
 
+  auto store_b = [&](int st) { store_b_rows(st, 0, B_LD); };
+
   f32x16 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
@@ -219,42 +261,88 @@ qgemm_kernel(KParams p)
     }
   }
 
-  if (nsteps > 0) {
-    load_tiles(kbeg);
-    store_tiles(0);
-    __syncthreads();
-    for (int s = 0; s < nsteps; ++s) {
-      const int st = s & 1;
-      const bool more = s + 1 < nsteps;
-      if (more) { load_tiles(kbeg + (s + 1) * kBK); }
-      const uint16_t* la = lds_a[st] + (wm * WTM + (lane & 31)) * kLdsRow +
-                           (lane >> 5) * 8;
-      const uint16_t* lb = lds_b[st] + (wn * WTN + (lane & 31)) * kLdsRow +
-                           (lane >> 5) * 8;
+  // Fragment registers, double-buffered across the four 16-deep K slices
+  // of a step: slice kk+1 is read from LDS while slice kk's MFMAs run.
+  bf16x8 afr[2][FM];
+  bf16x8 bfr[2][FN];
+  const int a_frag = (wm * WTM + (lane & 31)) * kLdsRow + (lane >> 5) * 8;
+  const int b_frag = (wn * WTN + (lane & 31)) * kLdsRow + (lane >> 5) * 8;
+
+  auto read_frags = [&](int st, int kk, int buf) {
 #pragma unroll
-      for (int kk = 0; kk < kBK / 16; ++kk) {
-        bf16x8 af[FM];
-        bf16x8 bfv[FN];
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-          af[i] = *(const bf16x8*)(la + i * 32 * kLdsRow + kk * 16);
-        }
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          bfv[j] = *(const bf16x8*)(lb + j * 32 * kLdsRow + kk * 16);
-        }
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-#pragma unroll
-          for (int j = 0; j < FN; ++j) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                af[i], bfv[j], acc[i][j], 0, 0, 0);
-          }
-        }
-      }
-      if (more) { store_tiles(st ^ 1); }
-      __syncthreads();
+    for (int i = 0; i < FM; ++i) {
+      afr[buf][i] = *(const bf16x8*)(lds_a[st] + a_frag + i * 32 * kLdsRow + kk * 16);
     }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      bfr[buf][j] = *(const bf16x8*)(lds_b[st] + b_frag + j * 32 * kLdsRow + kk * 16);
+    }
+  };
+  auto mfma_all = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr[buf][i], bfr[buf][j],
+                                                           acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+
+  // One K step from LDS stage s&1, in four 16-deep slices. Interleaved with
+  // the slices' MFMAs it writes step s+1 (already in registers) to the other
+  // stage -- X tiles as they are, weight tiles dequantized -- and fetches
+  // step s+2 into the registers just freed, so each global load has about a
+  // step to land. The step's one barrier sits before the last slice, whose
+  // fragments are already in registers; the next step's first fragments are
+  // read under that slice's MFMAs. sched_barrier fences keep each chunk's
+  // mix of MFMA, LDS, VALU and VMEM work together.
+  auto step = [&](int s, auto do_store, auto do_load) {
+    constexpr bool kStore = decltype(do_store)::value;
+    constexpr bool kLoad = decltype(do_load)::value;
+    constexpr int b1 = B_LD / 4;
+    constexpr int b2 = (3 * B_LD) / 4;
+    const int st = s & 1;
+    const int nst = st ^ 1;
+    read_frags(st, 1, 1);
+    mfma_all(0);
+    if constexpr (kStore) {
+      store_a(nst);
+      store_b_rows(nst, 0, b1);
+    }
+    if constexpr (kLoad) { load_a(kbeg + (s + 2) * kBK); }
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(st, 2, 0);
+    mfma_all(1);
+    if constexpr (kStore) { store_b_rows(nst, b1, b2); }
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(st, 3, 1);
+    mfma_all(0);
+    if constexpr (kStore) { store_b_rows(nst, b2, B_LD); }
+    if constexpr (kLoad) { load_b(kbeg + (s + 2) * kBK); }
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    if constexpr (kStore) { read_frags(nst, 0, 0); }
+    mfma_all(1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Two LDS stages; the last two steps are peeled so that the steady-state
+  // body has no branches.
+  if (nsteps > 0) {
+    load_regs(kbeg);
+    store_a(0);
+    store_b(0);
+    if (nsteps > 1) { load_regs(kbeg + kBK); }
+    __syncthreads();
+    read_frags(0, 0, 0);
+    int s = 0;
+    for (; s + 2 < nsteps; ++s) { step(s, std::true_type{}, std::true_type{}); }
+    if (s + 1 < nsteps) {
+      step(s, std::true_type{}, std::false_type{});
+      ++s;
+    }
+    step(s, std::false_type{}, std::false_type{});
   }
 
   // Accumulator layout of the 32x32 f32 MFMA result: lane l, register r
