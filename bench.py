@@ -443,7 +443,7 @@ def main():
         "pct_bf16_peak": round(100 * ffn["tflops"] / PEAK_BF16_TFLOPS, 2),
         "ffn": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in ffn.items()},
         "roofline": {
-            "kernel": "qgemm_kernel<256,256,2,2,8,false> (up with GELU and down)",
+            "kernel": "qgemm_kernel<256,256,2,4,8,false> (up with GELU and down)",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,

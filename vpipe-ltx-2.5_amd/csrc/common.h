@@ -37,12 +37,18 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f)
 
 // GELU, tanh approximation: 0.5 x (1 + tanh(u)) with
 // u = sqrt(2/pi) (x + 0.044715 x^3), evaluated through the identity
-// 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)). Saturates correctly at both
-// ends: exp overflow gives x / inf = -0 for large negative x.
+// 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)) = 1 / (1 + 2^z),
+// z = x (k1 + k3 x^2), k1 = -2 sqrt(2/pi) log2(e), k3 = 0.044715 k1:
+// five VALU ops plus the hardware exp2 and reciprocal (each within about
+// 1 ulp of f32, far inside the bf16 rounding that follows). Saturates at
+// both ends: 2^z overflows to inf for large negative x, giving
+// x * rcp(inf) = -0; for large positive x, 2^z = 0 and the result is x.
 __device__ __forceinline__ float gelu_tanh(float x)
 {
-  const float u = 0.7978845608028654f * fmaf(0.044715f * x, x * x, x);
-  return x / (1.0f + __expf(-2.0f * u));
+  constexpr float k1 = -2.302208198144325f;
+  constexpr float k3 = -0.1029432395800235f;
+  const float z = x * fmaf(k3, x * x, k1);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
 }
 
 // ---- internal launcher interface ------------------------------------------

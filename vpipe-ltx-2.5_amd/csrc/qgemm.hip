@@ -3,8 +3,10 @@
 // One kernel template serves every weight format (w8 / w4 group-affine
 // codes, or dense bf16) and both tile shapes:
 //
-//   tall   BM x BN = 256 x 256, 4 waves in 2 x 2, 128 x 128 per wave
-//          (the video GEMMs, thousands of tokens)
+//   tall   BM x BN = 256 x 256, 8 waves in 2 x 4, 128 x 64 per wave
+//          (the video GEMMs, thousands of tokens); two waves per SIMD,
+//          so one wave's LDS / barrier / load waits are covered by the
+//          other's MFMAs
 //   skinny BM x BN = 128 x 128, 4 waves in 2 x 2, 64 x 64 per wave,
 //          with split-K across workgroups (the audio GEMMs at ~126 tokens
 //          and anything else too small to fill 256 CUs)
@@ -30,11 +32,14 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 namespace ltx25 {
 namespace {
 
-constexpr int kThreads = 256;
+// Wave grid of the 256 x 256 tile.
+constexpr int kTallWM = 2;
+constexpr int kTallWN = 4;
 constexpr int kBK = 64;             // K per main-loop step
 constexpr int kLdsRow = kBK + 8;    // bf16 per LDS row: 144 B pitch keeps
                                     // the 16 B fragment reads conflict-free
@@ -108,21 +113,56 @@ __device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r,
   return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
 }
 
+// Instruction-issue pattern for one scheduling region of NM MFMAs: after
+// each MFMA, one LDS read while any of the NR remain, then this gap's share
+// of the NG global loads and NV VALU ops, and an LDS write every other gap
+// over the last 2*NW gaps (the writes depend on the VALU work before them).
+// Masks: 0x008 MFMA, 0x100 LDS read, 0x200 LDS write, 0x020 VMEM read,
+// 0x002 VALU.
+template <int I, int NM, int NR, int NW, int NV, int NG>
+__device__ __forceinline__ void interleave_gap()
+{
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  constexpr int r = I < NR ? 1 : 0;
+  constexpr int g = (I + 1) * NG / NM - I * NG / NM;
+  constexpr int v = (I + 1) * NV / NM - I * NV / NM;
+  constexpr int w0 = NM - 2 * NW > 0 ? NM - 2 * NW : 0;
+  constexpr int w = (I >= w0 && ((I - w0) & 1) == 0 && (I - w0) / 2 < NW) ? 1 : 0;
+  if constexpr (r > 0) { __builtin_amdgcn_sched_group_barrier(0x100, r, 0); }
+  if constexpr (g > 0) { __builtin_amdgcn_sched_group_barrier(0x020, g, 0); }
+  if constexpr (v > 0) { __builtin_amdgcn_sched_group_barrier(0x002, v, 0); }
+  if constexpr (w > 0) { __builtin_amdgcn_sched_group_barrier(0x200, w, 0); }
+}
+
+template <int NM, int NR, int NW, int NV, int NG, int... I>
+__device__ __forceinline__ void interleave_seq(std::integer_sequence<int, I...>)
+{
+  (interleave_gap<I, NM, NR, NW, NV, NG>(), ...);
+}
+
+template <int NM, int NR, int NW, int NV, int NG>
+__device__ __forceinline__ void interleave()
+{
+  interleave_seq<NM, NR, NW, NV, NG>(std::make_integer_sequence<int, NM>{});
+}
+
 template <int BM, int BN, int WM, int WN, int BITS, bool SPLIT>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(WM * WN * 64)
 qgemm_kernel(KParams p)
 {
+  constexpr int NT = WM * WN * 64;                   // threads
   constexpr int WTM = BM / WM;
   constexpr int WTN = BN / WN;
   constexpr int FM = WTM / 32;
   constexpr int FN = WTN / 32;
-  constexpr int A_LD = BM * 8 / kThreads;            // 16 B chunks / thread
+  constexpr int A_LD = BM * 8 / NT;                  // 16 B chunks / thread
+  constexpr int A_RSTEP = NT / 8;
   constexpr int B_CPR = BITS == 16 ? 8 : kBK * BITS / 8 / 16;  // chunks/row
-  constexpr int B_LD = BN * B_CPR / kThreads;
-  constexpr int B_RSTEP = kThreads / B_CPR;
+  constexpr int B_LD = BN * B_CPR / NT;
+  constexpr int B_RSTEP = NT / B_CPR;
   constexpr int CPC = BITS == 16 ? 8 : 128 / BITS;   // codes per chunk
   constexpr bool QUANT = BITS != 16;
-  static_assert(A_LD >= 1 && B_LD >= 1, "tile too small for 256 threads");
+  static_assert(A_LD >= 1 && B_LD >= 1, "tile too small for the thread count");
 
   __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * kLdsRow];
   __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][BN * kLdsRow];
@@ -160,7 +200,7 @@ qgemm_kernel(KParams p)
   uint32_t s_off[B_LD];
 #pragma unroll
   for (int i = 0; i < A_LD; ++i) {
-    a_off[i] = (uint32_t)(((size_t)(m0 + a_r + 32 * i) * p.K + a_c * 8) * 2);
+    a_off[i] = (uint32_t)(((size_t)(m0 + a_r + A_RSTEP * i) * p.K + a_c * 8) * 2);
   }
 #pragma unroll
   for (int i = 0; i < B_LD; ++i) {
@@ -197,7 +237,7 @@ qgemm_kernel(KParams p)
   auto store_a = [&](int st) {
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
-      *(uint4*)&lds_a[st][(a_r + 32 * i) * kLdsRow + a_c * 8] = areg[i];
+      *(uint4*)&lds_a[st][(a_r + A_RSTEP * i) * kLdsRow + a_c * 8] = areg[i];
     }
   };
 
@@ -291,39 +331,54 @@ qgemm_kernel(KParams p)
 
   // One K step from LDS stage s&1, in four 16-deep slices. Interleaved with
   // the slices' MFMAs it writes step s+1 (already in registers) to the other
-  // stage -- X tiles as they are, weight tiles dequantized -- and fetches
-  // step s+2 into the registers just freed, so each global load has about a
-  // step to land. The step's one barrier sits before the last slice, whose
-  // fragments are already in registers; the next step's first fragments are
-  // read under that slice's MFMAs. sched_barrier fences keep each chunk's
-  // mix of MFMA, LDS, VALU and VMEM work together.
+  // stage -- X tiles as they are in slice 0, weight tiles dequantized in
+  // slices 1 and 2 -- and fetches step s+2 into the registers just freed
+  // (X in slice 1, weights in slice 2), so each global load has about a
+  // step to land. Every slice also reads the next slice's fragments, so the
+  // fragment registers are double-buffered. The step's one barrier sits
+  // before the last slice, whose fragments are already in registers; the
+  // next step's first fragments are read under that slice's MFMAs.
+  //
+  // Each slice is its own scheduling region (sched_barrier) with an explicit
+  // issue pattern (interleave<>): one MFMA per gap, the fragment reads in the
+  // first gaps, the VALU dequant and global loads spread over all gaps, the
+  // LDS writes in the second half. Left to itself the scheduler clusters
+  // the reads after the MFMAs that free their registers, and the wave then
+  // waits on LDS latency with the matrix pipe idle.
+  constexpr int kMf = FM * FN;
+  constexpr int kRd = FM + FN;
+  constexpr int kB1 = B_LD / 2;
+  constexpr int kValuChunk = !QUANT ? 0 : (BITS == 8 ? 42 : 86);
+  constexpr int kWrChunk = !QUANT ? 1 : (BITS == 8 ? 2 : 4);
   auto step = [&](int s, auto do_store, auto do_load) {
     constexpr bool kStore = decltype(do_store)::value;
     constexpr bool kLoad = decltype(do_load)::value;
-    constexpr int b1 = B_LD / 4;
-    constexpr int b2 = (3 * B_LD) / 4;
+    constexpr int kGlB = QUANT ? 3 * B_LD : B_LD;
     const int st = s & 1;
     const int nst = st ^ 1;
     read_frags(st, 1, 1);
     mfma_all(0);
-    if constexpr (kStore) {
-      store_a(nst);
-      store_b_rows(nst, 0, b1);
-    }
-    if constexpr (kLoad) { load_a(kbeg + (s + 2) * kBK); }
+    if constexpr (kStore) { store_a(nst); }
+    interleave<kMf, kRd, kStore ? A_LD : 0, 0, 0>();
     __builtin_amdgcn_sched_barrier(0);
     read_frags(st, 2, 0);
     mfma_all(1);
-    if constexpr (kStore) { store_b_rows(nst, b1, b2); }
+    if constexpr (kStore) { store_b_rows(nst, 0, kB1); }
+    if constexpr (kLoad) { load_a(kbeg + (s + 2) * kBK); }
+    interleave<kMf, kRd, kStore ? kB1 * kWrChunk : 0, kStore ? kB1 * kValuChunk : 0,
+               kLoad ? A_LD : 0>();
     __builtin_amdgcn_sched_barrier(0);
     read_frags(st, 3, 1);
     mfma_all(0);
-    if constexpr (kStore) { store_b_rows(nst, b2, B_LD); }
+    if constexpr (kStore) { store_b_rows(nst, kB1, B_LD); }
     if constexpr (kLoad) { load_b(kbeg + (s + 2) * kBK); }
+    interleave<kMf, kRd, kStore ? (B_LD - kB1) * kWrChunk : 0,
+               kStore ? (B_LD - kB1) * kValuChunk : 0, kLoad ? kGlB : 0>();
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     if constexpr (kStore) { read_frags(nst, 0, 0); }
     mfma_all(1);
+    interleave<kMf, kStore ? kRd : 0, 0, 0, 0>();
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -409,30 +464,30 @@ splitk_reduce_kernel(const float* partial, int splits, const void* bias,
   }
 }
 
-template <int BM, int BN, int BITS, bool SPLIT>
+template <int BM, int BN, int WM, int WN, int BITS, bool SPLIT>
 hipError_t launch_cfg(const KParams& kp, int splits, hipStream_t stream)
 {
   const dim3 grid((unsigned)(kp.tiles_m * kp.tiles_n), (unsigned)splits, 1);
-  hipLaunchKernelGGL((qgemm_kernel<BM, BN, 2, 2, BITS, SPLIT>), grid,
-                     dim3(kThreads), 0, stream, kp);
+  hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, BITS, SPLIT>), grid,
+                     dim3(WM * WN * 64), 0, stream, kp);
   return hipGetLastError();
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int WM, int WN>
 hipError_t launch_tile(const KParams& kp, int bits, int splits,
                        hipStream_t stream)
 {
   const bool split = splits > 1;
   switch (bits) {
     case 8:
-      return split ? launch_cfg<BM, BN, 8, true>(kp, splits, stream)
-                   : launch_cfg<BM, BN, 8, false>(kp, splits, stream);
+      return split ? launch_cfg<BM, BN, WM, WN, 8, true>(kp, splits, stream)
+                   : launch_cfg<BM, BN, WM, WN, 8, false>(kp, splits, stream);
     case 4:
-      return split ? launch_cfg<BM, BN, 4, true>(kp, splits, stream)
-                   : launch_cfg<BM, BN, 4, false>(kp, splits, stream);
+      return split ? launch_cfg<BM, BN, WM, WN, 4, true>(kp, splits, stream)
+                   : launch_cfg<BM, BN, WM, WN, 4, false>(kp, splits, stream);
     default:
-      return split ? launch_cfg<BM, BN, 16, true>(kp, splits, stream)
-                   : launch_cfg<BM, BN, 16, false>(kp, splits, stream);
+      return split ? launch_cfg<BM, BN, WM, WN, 16, true>(kp, splits, stream)
+                   : launch_cfg<BM, BN, WM, WN, 16, false>(kp, splits, stream);
   }
 }
 
@@ -494,8 +549,8 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
   kp.tiles_n = (d.N + bn - 1) / bn;
 
   hipError_t e = plan.tile == 0
-                     ? launch_tile<256, 256>(kp, d.bits, plan.splits, stream)
-                     : launch_tile<128, 128>(kp, d.bits, plan.splits, stream);
+                     ? launch_tile<256, 256, kTallWM, kTallWN>(kp, d.bits, plan.splits, stream)
+                     : launch_tile<128, 128, 2, 2>(kp, d.bits, plan.splits, stream);
   if (e != hipSuccess || plan.splits <= 1) { return e; }
   const size_t total = (size_t)d.M * d.N;
   const unsigned blocks = (unsigned)((total + 1023) / 1024);
