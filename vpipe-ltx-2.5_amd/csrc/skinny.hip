@@ -2,27 +2,29 @@
 // stream's ~126 tokens): y = x . dequant(W)^T (+ bias) (+ GELU).
 //
 // These GEMMs sit near the bf16 ridge (about 256 FLOP per weight byte
-// against a ridge of about 300), so the weight stream from HBM and the
-// MFMA work both have to run near their peaks at once. The layout:
+// against a ridge of about 300) and each moves only 5-20 MB, so what
+// decides their speed is how much of the weight stream is in flight
+// against a loaded memory latency of 2-3 us. The layout:
 //
-//   - Each wave owns 32 output columns for ALL rows (up to 128 = four
-//     32-row v_mfma_f32_32x32x16_bf16 tiles). Every weight element is
-//     therefore dequantized exactly once, in registers, straight from its
-//     16-byte global load: weights never touch LDS.
-//   - The workgroup's NW waves cover BN = 32*NW adjacent columns and share
-//     the activation tile, staged through LDS one 64-deep K step at a time.
-//   - Lane l of a wave loads the 32 consecutive codes [32h, 32h+32) of a
-//     step for column l%32 (h = l/32). MFMA slice j uses codes
-//     [32h+8j, 32h+8j+8): the K order inside a step is permuted the same
-//     way for the activation fragments, which the dot product allows.
-//   - Weight loads run kDepth steps ahead in a register ring, so each
-//     wave keeps about kDepth * 2 KB of the weight stream in flight.
-//   - K is split over `splits` workgroups per column tile. Each writes an
-//     f32 partial tile; the last to arrive (an atomic counter per tile)
-//     sums the partials in split order, adds the bias, applies GELU and
-//     rounds once to bf16 -- deterministic, and the linear is one launch.
-//     The counter is reset by that last workgroup, so the counters are
-//     zero again when the launch ends.
+//   - A workgroup owns 128 output columns (4 waves x 32) and one K range
+//     (k_chunk, 256 or 512) of all rows. Its activation slab, 128 rows x
+//     k_chunk bf16, is loaded ONCE into LDS by direct global-to-LDS loads,
+//     behind a single barrier; the main loop then has no barrier at all.
+//   - Each wave streams only its own 32 weight columns, straight into
+//     registers in the MFMA operand layout, kSkDepth = 8 K steps (of 64)
+//     ahead. Lane l holds column l%32 and, per step, the 32 codes
+//     [32h, 32h+32) (h = l/32); MFMA slice j uses codes [32h+8j, +8), and
+//     the activation fragments use the same permutation of K, which the
+//     dot product allows. Every weight element is dequantized exactly once,
+//     in registers, w = bf16(fma(scale, q, zero point)), right in front of
+//     v_mfma_f32_32x32x16_bf16 (four 32-row tiles per wave).
+//   - K is split over `splits` workgroups. Each wave writes its f32
+//     partial 128 x 32 block and counts in on that block's own counter; the
+//     wave that arrives last sums the partials in split order, adds the
+//     bias, applies GELU and rounds once to bf16. The result is
+//     deterministic, the linear is one launch, and the reductions are
+//     spread over as many CUs as there are 32-column blocks. The last wave
+//     resets its counter, so the counters are zero again after the launch.
 //
 // Reference semantics: MetalOps::linear(QWeight) (src/ltx25-metal-ops.cc:
 // 531-569) over the affine_dequant weight, then ltx_bias_add.
@@ -33,10 +35,14 @@
 namespace ltx25 {
 namespace {
 
-constexpr int kSkBK = 64;                 // K per step
+typedef uint32_t __attribute__((address_space(3))) lds_u32;
+
 constexpr int kSkRows = 128;              // rows per workgroup
-constexpr int kSkLdsRow = kSkBK + 8;      // bf16 pitch of an activation row (144 B)
-constexpr int kSkDepth = 4;               // weight steps in flight per wave
+constexpr int kSkBK = 64;                 // K per step
+constexpr int kSkDepth = 8;               // weight steps in flight per wave
+constexpr int kSkWaves = 4;               // waves (32 columns each) per workgroup
+constexpr int kSysCoherent = 17;          // buffer cache policy sc0 | sc1
+constexpr uint32_t kOob = 0x80000000u;    // a per-lane offset past every buffer
 
 struct SkParams {
   const uint16_t* x;
@@ -46,16 +52,17 @@ struct SkParams {
   const void* bias;
   uint16_t* y;
   float* partial;        // [splits][M][N] f32
-  int* counters;         // [tiles_n], zero between launches
+  int* counters;         // [tiles_n * kSkWaves], zero between launches
   int M, N, K;
   int gshift, gcols;
-  int k_chunk, splits;
+  int k_chunk, splits;   // k_chunk is 256 or 512
   int bias_type, epilogue;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const void* p, size_t bytes)
 {
-  // Raw buffer: loads past `bytes` return zeros (rows past M, columns past N).
+  // Raw buffer: the range check on the per-lane offset returns zeros (and
+  // drops stores) past `bytes` without a memory access.
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
                                            (int)(uint32_t)bytes, 0x00020000);
 }
@@ -99,23 +106,19 @@ __device__ __forceinline__ bf16x8 dequant8(const uint32_t* words, float s, float
   return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-template <int NW, int BITS>
-__global__ void __launch_bounds__(NW * 64)
+template <int BITS>
+__global__ void __launch_bounds__(kSkWaves * 64)
 skinny_kernel(SkParams p)
 {
   constexpr bool QUANT = BITS != 16;
-  constexpr int WB = QUANT ? 32 * BITS / 8 : 64;        // weight bytes per lane per step
-  constexpr int WL = WB / 16;                            // 16 B loads per lane per step
-  constexpr int WLOADS = WL + (QUANT ? 2 : 0);           // + scale and zero point
-  constexpr int NT = NW * 64;
-  constexpr int XL = kSkRows * kSkBK * 2 / 16 / NT;      // activation 16 B loads per thread per step
-  static_assert(XL >= 1, "too many threads for one activation tile");
+  constexpr int WB = QUANT ? 32 * BITS / 8 : 64;   // weight bytes per lane per step
+  constexpr int WL = WB / 16;                       // 16 B loads per lane per step
 
-  // The activation tile of a step, 128 rows x 64 bf16, in two LDS stages
-  // with a 144 B row pitch: the 16 B fragment reads of 16 rows at one
-  // column then hit 16 distinct bank groups.
-  __shared__ __attribute__((aligned(16))) uint16_t lds_x[2][kSkRows * kSkLdsRow];
-  __shared__ int s_last;
+  // The activation slab: 128 rows of k_chunk bf16 (512 B or 1 KB), rows
+  // unpadded so that direct loads (64 lanes x 16 B = 1 KB contiguous) fill
+  // it. The 16 B chunk c of row r sits at position c ^ (r & 15), so a
+  // fragment read (16 rows, one chunk) hits 16 distinct bank groups.
+  extern __shared__ __attribute__((aligned(1024))) uint16_t lds_x[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -123,10 +126,12 @@ skinny_kernel(SkParams p)
   const int half = lane >> 5;
   const int tn = blockIdx.x;
   const int split = blockIdx.y;
-  const int col = tn * 32 * NW + wave * 32 + (lane & 31);
+  const int col = tn * 32 * kSkWaves + wave * 32 + (lane & 31);
+  const bool in_n = col < p.N;
   const int kbeg = split * p.k_chunk;
   const int kend = min(p.K, kbeg + p.k_chunk);
   const int nsteps = (kend - kbeg) / kSkBK;
+  const int rowb = p.k_chunk * 2;
 
   const size_t row_bytes = (size_t)p.K * (QUANT ? BITS : 16) / 8;
   const __amdgpu_buffer_rsrc_t xr = sk_rsrc(p.x, (size_t)p.M * p.K * 2);
@@ -134,72 +139,72 @@ skinny_kernel(SkParams p)
   const __amdgpu_buffer_rsrc_t sr = sk_rsrc(p.scales, QUANT ? (size_t)p.N * p.gcols * 2 : 0);
   const __amdgpu_buffer_rsrc_t qr = sk_rsrc(p.qbias, QUANT ? (size_t)p.N * p.gcols * 2 : 0);
 
-  // Steps at or past nsteps load with a per-lane offset (voffset) past
-  // every buffer's end: the buffer unit's range check returns zeros
-  // without touching memory, and the zero codes (scale and zero point 0)
-  // dequantize to 0 and add nothing. The range check covers the per-lane
-  // offset, so every offset that can leave a buffer rides there; the
-  // uniform offset (soffset) is only used in range. Every step therefore
-  // issues the same loads with no branch, and load counts stay exact.
-  constexpr uint32_t kOob = 0x80000000u;
-  auto k_of = [&](int s) { return (uint32_t)(kbeg + s * kSkBK); };
-
-  // Weight stream: lane l loads the 32 codes [32h, 32h+32) of a step for
-  // column l%32 (h = l/32) into a register ring kSkDepth steps deep.
+  // Weight ring: slot d holds step s (s % kSkDepth == d) from its load
+  // until it is computed. Steps past nsteps, and columns past N, load with
+  // an out-of-range per-lane offset: zeros, no memory access, and the zero
+  // codes with zero scale and zero point add nothing. The uniform K offset
+  // rides in soffset only when in range (the range check covers the
+  // per-lane offset). Every step issues the same loads with no branch.
   const uint32_t w_off = (uint32_t)((size_t)col * row_bytes + (size_t)half * WB);
   const uint32_t s_off =
       QUANT ? (uint32_t)(((size_t)col * p.gcols + ((32 * half) >> p.gshift)) * 2) : 0u;
   uint4 wreg[kSkDepth][WL];
   uint16_t sreg[kSkDepth];
   uint16_t qreg[kSkDepth];
+  // soffset must be wave-uniform (a per-lane value would make the compiler
+  // loop over its distinct values), so it depends only on the step.
   auto load_w = [&](int s, int d) {
-    const bool in = s < nsteps;
-    const uint32_t wo = in ? (uint32_t)((size_t)k_of(s) * (QUANT ? BITS : 16) / 8) : 0u;
+    const bool step_in = s < nsteps;
+    const bool in = step_in && in_n;
+    const uint32_t k = (uint32_t)(kbeg + s * kSkBK);
+    const uint32_t wo = step_in ? (uint32_t)((size_t)k * (QUANT ? BITS : 16) / 8) : 0u;
 #pragma unroll
     for (int i = 0; i < WL; ++i) { wreg[d][i] = sk_load16(wr, in ? w_off + 16 * i : kOob, wo); }
     if constexpr (QUANT) {
-      const uint32_t so = in ? (k_of(s) >> p.gshift) * 2 : 0u;
+      const uint32_t so = step_in ? (k >> p.gshift) * 2 : 0u;
       const uint32_t vo = in ? s_off : kOob;
       sreg[d] = __builtin_amdgcn_raw_buffer_load_b16(sr, (int)vo, (int)so, 0);
       qreg[d] = __builtin_amdgcn_raw_buffer_load_b16(qr, (int)vo, (int)so, 0);
     }
   };
 
-  // Activation stream: each thread loads XL 16 B chunks of the 128 x 64
-  // tile into a register ring kSkDepth steps deep and writes them to LDS
-  // one step before they are read. vmcnt retires a wave's loads in issue
-  // order, so waiting for an activation step also waits for every weight
-  // load issued before it: the activation loads therefore run as far ahead
-  // as the weight loads, and each step issues them first.
-  uint32_t x_off[XL];
-  int x_lds[XL];
 #pragma unroll
-  for (int i = 0; i < XL; ++i) {
-    const int c = tid + NT * i;
-    const int r = c >> 3;
-    const int kc = c & 7;
-    x_off[i] = (uint32_t)(((size_t)r * p.K + kc * 8) * 2);
-    x_lds[i] = r * kSkLdsRow + kc * 8;
-  }
-  uint4 xreg[kSkDepth][XL];
-  auto load_x = [&](int s, int slot) {
-    const bool in = s < nsteps;
-    const uint32_t kb = in ? k_of(s) * 2 : 0u;
-#pragma unroll
-    for (int i = 0; i < XL; ++i) { xreg[slot][i] = sk_load16(xr, in ? x_off[i] : kOob, kb); }
-  };
-  auto store_x = [&](int st, int slot) {
-#pragma unroll
-    for (int i = 0; i < XL; ++i) { *(uint4*)&lds_x[st][x_lds[i]] = xreg[slot][i]; }
-  };
+  for (int d = 0; d < kSkDepth; ++d) { load_w(d, d); }
 
-  // Fragment reads: tile i, slice j reads row 32i + l%32 at k = 32h + 8j.
-  const uint16_t* a_base = &lds_x[0][0] + (lane & 31) * kSkLdsRow + 32 * half;
-  auto read_a = [&](int st, int j, bf16x8* af) {
-    const uint16_t* b = a_base + st * kSkRows * kSkLdsRow + 8 * j;
+  // The slab: 1 KB direct load g covers LDS bytes [1024 g, 1024 g + 1024);
+  // lane i lands at byte 16 i of it, i.e. row r, position pos, and fetches
+  // the row's chunk pos ^ (r & 15). Chunks past this split's K range (the
+  // last split) or rows past M read as zero.
+  {
+    const int n_loads = kSkRows * rowb / 1024;
+    const int per_wave = n_loads / kSkWaves;
+    for (int q = 0; q < per_wave; ++q) {
+      const int g = wave * per_wave + q;
+      const int byte = 1024 * g + 16 * lane;
+      const int r = byte / rowb;
+      const int c = ((byte % rowb) / 16) ^ (r & 15);
+      const int k = kbeg + 8 * c;
+      const uint32_t vo = k < kend ? (uint32_t)(((size_t)r * p.K + k) * 2) : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_u32*)(lds_x + 512 * g), 16, (int)vo,
+                                               0, 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // Fragment offsets: tile i, slice j of step s reads row 32i + l%32, chunk
+  // 8s + 4h + j, stored at position (8s + 4h + j) ^ (row & 15); since the
+  // XOR only touches the low 4 bits, step s adds 256 B per pair of steps
+  // and its parity picks one of two offset sets.
+  const int rsw = lane & 15;
+  const int arow_b = (lane & 31) * rowb;
+  int a_off[2][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { af[i] = *(const bf16x8*)(b + i * 32 * kSkLdsRow); }
-  };
+  for (int par = 0; par < 2; ++par) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { a_off[par][j] = arow_b + 16 * ((8 * par + 4 * half + j) ^ rsw); }
+  }
+  const char* slab = (const char*)lds_x;
 
   f32x16 acc[4];
 #pragma unroll
@@ -208,13 +213,11 @@ skinny_kernel(SkParams p)
     for (int r = 0; r < 16; ++r) { acc[i][r] = 0.0f; }
   }
 
-  // One step: slice 0's fragment reads, then the weight dequant (its VALU
-  // work covers the LDS latency), then per slice 4 MFMAs with the next
-  // slice's reads interleaved.
-  auto compute = [&](int st, int d) {
-    bf16x8 afr[2][4];
+  // One step: dequantize the slot's 32 codes into four B fragments, then
+  // 4 slices x 4 row tiles of MFMAs with the A fragments read one slice
+  // ahead.
+  auto compute = [&](int s, int d) {
     bf16x8 bfr[4];
-    read_a(st, 0, afr[0]);
     if constexpr (QUANT) {
       const float sc = bf16_to_f32(sreg[d]);
       const float qb = bf16_to_f32(qreg[d]);
@@ -225,42 +228,35 @@ skinny_kernel(SkParams p)
 #pragma unroll
       for (int j = 0; j < 4; ++j) { bfr[j] = __builtin_bit_cast(bf16x8, wreg[d][j]); }
     }
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, QUANT ? 20 * 4 : 0, 0);
+    const char* base = slab + 256 * (s >> 1);
+    const int par = d & 1;
+    bf16x8 afr[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      afr[0][i] = *(const bf16x8*)(base + a_off[par][0] + i * 32 * rowb);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (j < 3) { read_a(st, j + 1, afr[(j + 1) & 1]); }
+      if (j < 3) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          afr[(j + 1) & 1][i] = *(const bf16x8*)(base + a_off[par][j + 1] + i * 32 * rowb);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr[j & 1][i], bfr[j], acc[i], 0, 0, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (j < 3) { __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); }
       }
     }
   };
 
-  // Step s reads LDS stage s&1 and ring slot s%D; then it loads
-  // activation step s+D and weight step s+D into that slot, writes
-  // activation step s+1 (loaded three steps ago) to the other LDS stage,
-  // and meets the other waves at the barrier, which publishes that stage
-  // (the previous barrier guarantees every wave is done reading it). Up to
-  // D-1 padded steps at the end compute zeros.
-#pragma unroll
-  for (int d = 0; d < kSkDepth; ++d) {
-    load_x(d, d);
-    load_w(d, d);
-  }
-  store_x(0, 0);
-  __syncthreads();
+  // Up to kSkDepth - 1 padded steps at the end compute zeros.
   for (int s0 = 0; s0 < nsteps; s0 += kSkDepth) {
 #pragma unroll
     for (int d = 0; d < kSkDepth; ++d) {
       const int s = s0 + d;
-      compute(d & 1, d);
-      load_x(s + kSkDepth, d);
+      compute(s, d);
       load_w(s + kSkDepth, d);
-      store_x((d + 1) & 1, (d + 1) % kSkDepth);
-      __syncthreads();
     }
   }
 
@@ -269,7 +265,6 @@ skinny_kernel(SkParams p)
   // buffer resources sized to the output: rows past M fall past the end,
   // and columns past N get an out-of-range per-lane offset, so masked
   // elements are dropped by the range check instead of branched around.
-  const bool in_n = col < p.N;
   auto row_of = [&](int i, int r) { return 32 * i + 8 * (r >> 2) + 4 * half + (r & 3); };
   auto finish = [&](const f32x16* v) {
     const __amdgpu_buffer_rsrc_t yr = sk_rsrc(p.y, (size_t)p.M * p.N * 2);
@@ -290,32 +285,38 @@ skinny_kernel(SkParams p)
     return;
   }
 
+  // Publish this wave's partial block, then count in on the block's
+  // counter. The partial stores write through to memory (system-coherent
+  // cache policy) and are waited for before the atomic; the last wave reads
+  // the partials back with the same policy, bypassing the caches that are
+  // not coherent across XCDs. (An agent-scope fence pair would instead
+  // write back and invalidate the whole L2 in every wave.)
   const size_t plane = (size_t)p.M * p.N;
   {
-    const __amdgpu_buffer_rsrc_t wr_p = sk_rsrc(p.partial + split * plane, plane * 4);
+    const __amdgpu_buffer_rsrc_t pw = sk_rsrc(p.partial + split * plane, plane * 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const uint32_t vo = in_n ? (uint32_t)(((size_t)row_of(i, r) * p.N + col) * 4) : kOob;
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][r]), wr_p,
-                                              (int)vo, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][r]), pw, (int)vo, 0,
+                                              kSysCoherent);
       }
     }
   }
-  // Publish the partial, then count this split in.
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) { s_last = atomicAdd(&p.counters[tn], 1) == p.splits - 1; }
-  __syncthreads();
-  if (!s_last) { return; }
-  __threadfence();
-  // Sum the partials in split order (this workgroup's own included, read
-  // back like the others, so the order never depends on who arrived
-  // last). Each split's plane is its own buffer resource: rows past M fall
-  // past its end and columns past N get an out-of-range per-lane offset,
-  // so the 64 loads per lane and split carry no branch, are issued
-  // together, and the reduction costs `splits` round trips.
+  __builtin_amdgcn_s_waitcnt(0);
+  int* counter = p.counters + tn * kSkWaves + wave;
+  int before = 0;
+  if (lane == 0) {
+    before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  before = __builtin_amdgcn_readfirstlane(before);
+  if (before != p.splits - 1) { return; }
+
+  // Last wave of the block: sum the partials in split order (its own read
+  // back like the others, so the order never depends on who arrived last).
+  // Each split's 64 values per lane are loaded together, so the reduction
+  // costs `splits` round trips.
   f32x16 sum[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -330,27 +331,39 @@ skinny_kernel(SkParams p)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const uint32_t vo = in_n ? (uint32_t)(((size_t)row_of(i, r) * p.N + col) * 4) : kOob;
-        v[i][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (int)vo, 0, 0));
+        v[i][r] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(pr, (int)vo, 0, kSysCoherent));
       }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) { sum[i] += v[i]; }
   }
   finish(sum);
-  if (tid == 0) { p.counters[tn] = 0; }
+  if (lane == 0) { *counter = 0; }
 }
 
-template <int NW>
-hipError_t launch_nw(const SkParams& kp, int bits, int tiles_n, hipStream_t stream)
+// The slab is dynamic LDS of up to 128 KB; a kernel may use more than
+// 64 KB of it only once the limit is raised for that kernel.
+template <int BITS>
+hipError_t launch_one(const SkParams& kp, dim3 grid, size_t lds, hipStream_t stream)
+{
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&skinny_kernel<BITS>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, kSkRows * 512 * 2);
+  if (attr != hipSuccess) { return attr; }
+  hipLaunchKernelGGL((skinny_kernel<BITS>), grid, dim3(kSkWaves * 64), lds, stream, kp);
+  return hipGetLastError();
+}
+
+hipError_t launch_bits(const SkParams& kp, int bits, int tiles_n, hipStream_t stream)
 {
   const dim3 grid((unsigned)tiles_n, (unsigned)kp.splits, 1);
-  const dim3 block(NW * 64);
+  const size_t lds = (size_t)kSkRows * kp.k_chunk * 2;
   switch (bits) {
-    case 8: hipLaunchKernelGGL((skinny_kernel<NW, 8>), grid, block, 0, stream, kp); break;
-    case 4: hipLaunchKernelGGL((skinny_kernel<NW, 4>), grid, block, 0, stream, kp); break;
-    default: hipLaunchKernelGGL((skinny_kernel<NW, 16>), grid, block, 0, stream, kp); break;
+    case 8: return launch_one<8>(kp, grid, lds, stream);
+    case 4: return launch_one<4>(kp, grid, lds, stream);
+    default: return launch_one<16>(kp, grid, lds, stream);
   }
-  return hipGetLastError();
 }
 
 int sk_ilog2(int v)
@@ -364,22 +377,18 @@ int sk_ilog2(int v)
 
 SkinnyPlan plan_skinny(int M, int N, int K, int cu_count)
 {
-  (void)M;
   SkinnyPlan plan;
-  // Column tiles of 32*waves; prefer 4 waves (the activation tile is then
-  // shared by 128 columns) and split K until about one workgroup per CU,
-  // keeping at least 4 steps of 64 per split.
-  plan.waves = 4;
-  const int tiles = (N + 32 * plan.waves - 1) / (32 * plan.waves);
-  const int max_split = std::max(1, K / 256);
-  int s = std::max(1, std::min(max_split, (cu_count + tiles - 1) / tiles));
-  int chunk = ((K + s - 1) / s + kSkBK - 1) / kSkBK * kSkBK;
-  s = (K + chunk - 1) / chunk;
+  plan.waves = kSkWaves;
+  const int tiles = (N + 32 * kSkWaves - 1) / (32 * kSkWaves);
+  // K splits of 512, or of 256 while that still leaves at most two
+  // workgroups per CU (the slab is then 64 KB and two share a CU).
+  const int chunk = (long)tiles * ((K + 255) / 256) <= 2L * cu_count ? 256 : 512;
+  const int s = (K + chunk - 1) / chunk;
   plan.splits = s;
   plan.k_chunk = chunk;
   plan.tiles_n = tiles;
   plan.workspace_bytes = s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
-  plan.counter_count = s > 1 ? tiles : 0;
+  plan.counter_count = s > 1 ? tiles * kSkWaves : 0;
   return plan;
 }
 
@@ -404,11 +413,7 @@ hipError_t launch_skinny(const GemmDesc& d, const SkinnyPlan& plan, float* parti
   kp.splits = plan.splits;
   kp.bias_type = d.bias != nullptr ? d.bias_type : kBiasNone;
   kp.epilogue = d.epilogue;
-  switch (plan.waves) {
-    case 1: return launch_nw<1>(kp, d.bits, plan.tiles_n, stream);
-    case 2: return launch_nw<2>(kp, d.bits, plan.tiles_n, stream);
-    default: return launch_nw<4>(kp, d.bits, plan.tiles_n, stream);
-  }
+  return launch_bits(kp, d.bits, plan.tiles_n, stream);
 }
 
 }  // namespace ltx25
