@@ -23,8 +23,11 @@ Also reported on the same line:
             reference's sources) timed on this host, 1 thread, on a row
             sample of the up-projection
 
+  lora      the LoRA delta at the FFN up shape, ranks 32 and 450, and
+  dequant_once  the dequant-once A/B arm against the fused kernel there
+
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip-cpu]
-                       [--skip-audio] [--skip-i8] [--skip-c4]
+                       [--skip-audio] [--skip-i8] [--skip-c4] [--skip-next]
 """
 import argparse
 import ctypes
@@ -200,6 +203,63 @@ def bench_audio(pkg, torch, steps, warmup, sets=6):
     }
 
 
+# ---- next rows: the LoRA delta and the dequant-once A/B arm ------------------------------
+def bench_lora(pkg, torch, steps, warmup):
+    """y += (x . A^T) . B^T at the video FFN shape with the x2 upscaler's rank 32 and the
+    distilled adapter's rank 450 (src/ltx25-lora.h): HBM-bound on x and y."""
+    M, K, N = 8160, 4096, 16384
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.randn((M, N), device="cuda", generator=g).to(torch.bfloat16)
+    out = {}
+    for rank in (32, 450):
+        a = (torch.randn((rank, K), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        b = (torch.randn((N, rank), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        fn = lambda: pkg.lora_add(x, a, b, y, M, K, N, rank)   # noqa: E731
+        for _ in range(warmup):
+            fn()
+        timer = EventTimer(torch)
+        for _ in range(steps):
+            timer.record("lora", fn)
+        torch.cuda.synchronize()
+        ms = timer.mean_ms("lora")
+        byt = M * K * 2 + rank * K * 2 + N * rank * 2 + 2 * M * N * 2
+        flop = 2.0 * M * rank * (K + N)
+        out[f"rank{rank}"] = {"us": ms * 1e3, "GBps": byt / (ms * 1e-3) / 1e9,
+                              "TFLOPs": flop / (ms * 1e-3) / 1e12,
+                              "frac_of_linear": None}
+    return out
+
+
+def bench_dequant_once(pkg, torch, steps, warmup):
+    """The A/B arm at the FFN up-projection: fused dequant-in-GEMM against expand-then-dense
+    (the reference's dequant_mma_ route), same shapes, same bits out."""
+    M, D, H = 8160, 4096, 16384
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    x = torch.randn((M, D), device="cuda", generator=g).to(torch.bfloat16)
+    w = make_qweight(pkg, torch, H, D, g)
+    h = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    res = {}
+    try:
+        for arm in (False, True):
+            pkg.set_dequant_once(arm)
+            fn = lambda: pkg.linear_q(x, w, None, h, M, D, H, pkg.EPI_GELU_TANH)  # noqa: E731
+            for _ in range(warmup):
+                fn()
+            timer = EventTimer(torch)
+            for _ in range(steps):
+                timer.record("up", fn)
+            torch.cuda.synchronize()
+            ms = timer.mean_ms("up")
+            res["dequant_once" if arm else "fused"] = {
+                "ms": ms, "TFLOPs": 2.0 * M * D * H / (ms * 1e-3) / 1e12}
+    finally:
+        pkg.set_dequant_once(False)
+    return res
+
+
 # ---- config 3: int8 GEMM ----------------------------------------------------------------
 def bench_i8(pkg, torch, steps, warmup):
     M, K = 8160, 4096
@@ -353,12 +413,86 @@ def cpu_baseline(rows=64):
     }
 
 
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "qgemm_ffn_hbm_traffic.json")
+COPY_BYTES = 256 << 20   # the --profile-copy kernel reads and writes this much
+
+
 def load_traffic():
-    p = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(p):
-        with open(p) as f:
+    if os.path.exists(TRAFFIC_JSON):
+        with open(TRAFFIC_JSON) as f:
             return json.load(f)
     return None
+
+
+def _pmc_rows(path):
+    import csv
+
+    out = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            out[int(r["Dispatch_Id"])] = (r["Kernel_Name"], int(r["Grid_Size"]),
+                                          float(r["Counter_Value"]))
+    return out
+
+
+def pmc_summary(fetch_csv, write_csv, cmd):
+    """HBM traffic per launch from two rocprofv3 --pmc runs of the same bench
+    command (FETCH_SIZE, then WRITE_SIZE; both KiB per dispatch), each scaled
+    by what the counter reads for the plain 256 MiB device copy that
+    --profile-copy adds (the last copy dispatch). Writes the markdown summary
+    and the JSON that the roofline's `traffic` field reads."""
+    fe, wr = _pmc_rows(fetch_csv), _pmc_rows(write_csv)
+    copies = [i for i, (n, _, _) in fe.items() if "copyBuffer" in n or "copy_kernel" in n]
+    big = [i for i in copies if fe[i][2] > 1000 and wr.get(i, ("", 0, 0))[2] > 1000]
+    if not big:
+        raise SystemExit("no calibration copy in the counter files (run with --profile-copy)")
+    cal = max(big)
+    f_fac = COPY_BYTES / (fe[cal][2] * 1024)
+    w_fac = COPY_BYTES / (wr[cal][2] * 1024)
+    groups = {}
+    for i, (name, grid, v) in fe.items():
+        if "qgemm_kernel" not in name and "splitk_reduce" not in name:
+            continue
+        short = name[name.index("ltx25::"):].split("(ltx25")[0].replace("(anonymous namespace)::", "")
+        g = groups.setdefault((short, grid), [0, 0.0, 0.0])
+        g[0] += 1
+        g[1] += v * 1024 * f_fac
+        g[2] += wr.get(i, ("", 0, 0.0))[2] * 1024 * w_fac
+    M, D, H = 8160, 4096, 16384
+    alg = {  # read, write bytes of the two FFN GEMMs
+        "up": (M * D * 2 + H * D + H * D // 64 * 4, M * H * 2),
+        "down": (M * H * 2 + D * H + D * H // 64 * 4, M * D * 2),
+    }
+    mt = (M + 255) // 256
+    ffn_grid = {mt * (H // 256) * 512: "up", mt * (D // 256) * 512: "down"}
+    lines = ["# HBM traffic per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE)", "",
+             "Commands (two counter runs of the same program, then this summary):", "",
+             "```", cmd, "```", "",
+             f"Calibration: the 256 MiB device copy (dispatch {cal}) reads "
+             f"{fe[cal][2]:.0f} KiB by FETCH_SIZE and writes {wr[cal][2]:.0f} KiB by WRITE_SIZE, "
+             f"so FETCH_SIZE is scaled by {f_fac:.3f} and WRITE_SIZE by {w_fac:.3f}.", "",
+             "| kernel | grid | launches | fetch MB/launch | write MB/launch | algorithmic read / write MB |",
+             "|---|---|---|---|---|---|"]
+    ffn = []
+    for (short, grid), (n, fb, wb) in sorted(groups.items(), key=lambda kv: -kv[1][1] / kv[1][0]):
+        which = ffn_grid.get(grid) if "256, 256" in short else None
+        a = f"{alg[which][0] / 1e6:.1f} / {alg[which][1] / 1e6:.1f} ({which})" if which else ""
+        lines.append(f"| `{short}` | {grid} | {n} | {fb / n / 1e6:.1f} | {wb / n / 1e6:.1f} | {a} |")
+        if which:
+            ffn.append(((fb + wb) / n, which))
+    traffic = sum(t for t, _ in ffn) / len(ffn) if ffn else None
+    alg_mean = sum(sum(alg[w]) for _, w in ffn) / len(ffn) if ffn else None
+    lines += ["", f"FFN GEMM (the roofline kernel, mean of up and down): "
+              f"{traffic / 1e6:.1f} MB per launch against {alg_mean / 1e6:.1f} MB algorithmic."
+              if traffic else "", ""]
+    with open(os.path.join(ROOT, "profiles", "qgemm_ffn_hbm_traffic.md"), "w") as f:
+        f.write("\n".join(lines))
+    with open(TRAFFIC_JSON, "w") as f:
+        json.dump({"traffic_bytes": round(traffic) if traffic else None,
+                   "algorithmic_bytes": round(alg_mean) if alg_mean else None,
+                   "fetch_factor": round(f_fac, 4), "write_factor": round(w_fac, 4),
+                   "source": "profiles/qgemm_ffn_hbm_traffic.md"}, f, indent=1)
+    print("\n".join(lines))
 
 
 def main():
@@ -370,10 +504,17 @@ def main():
     ap.add_argument("--skip-audio", action="store_true")
     ap.add_argument("--skip-i8", action="store_true")
     ap.add_argument("--skip-c4", action="store_true")
+    ap.add_argument("--skip-next", action="store_true",
+                    help="skip the LoRA-delta and dequant-once measurements")
     ap.add_argument("--profile-copy", action="store_true",
                     help="also run one plain 256 MiB device copy, the known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "CMD"),
+                    help="summarise two rocprofv3 --pmc counter files into profiles/ and exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: this build's path runs on a single MI355X; "
@@ -402,6 +543,16 @@ def main():
         log("int8 (config 3)")
         extra["i8"] = bench_i8(pkg, torch, args.steps, args.warmup)
         log(f"  {extra['i8']}")
+        torch.cuda.empty_cache()
+    if not args.skip_next:
+        log("LoRA delta and the dequant-once arm")
+        extra["lora"] = bench_lora(pkg, torch, max(5, args.steps // 2), args.warmup)
+        ffn_ms = ffn["up_ms"]
+        for v in extra["lora"].values():
+            v["frac_of_linear"] = v["us"] * 1e-3 / ffn_ms
+        extra["dequant_once"] = bench_dequant_once(pkg, torch, max(5, args.steps // 2),
+                                                   args.warmup)
+        log(f"  {extra['lora']}\n  {extra['dequant_once']}")
         torch.cuda.empty_cache()
     if not args.skip_c4:
         log("48-block linear set (config 4)")

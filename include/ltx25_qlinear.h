@@ -136,6 +136,42 @@ int ltx25_gelu_tanh(void* stream, const void* x, void* y, size_t n);
 int ltx25_dequant(void* stream, const ltx25_qweight* w, void* out_bf16,
                   int N, int K);
 
+/* Route quantized linears through the dequant-once arm (1) or the fused
+ * dequant-in-GEMM kernel (0, the default). The arm expands W into a
+ * grow-only bf16 [N][K] scratch shared across calls (the reference's
+ * `_w_deq`, src/ltx25-metal-ops.h:843-845) and runs the dense GEMM over it;
+ * the expansion equals the fused kernel's in-register dequant, so both arms
+ * return the same bits and differ only in speed and in 2 B per weight of
+ * extra traffic. Replaces the reference's dequant_mma_ route
+ * (src/ltx25-metal-ops.cc:467-502, tried first at :544) as an A/B hook. */
+int ltx25_set_dequant_once(int on);
+
+/* 1 when ltx25_linear_q would take the dequant-once arm for this shape:
+ * the arm is on, M >= 64 and N >= 16 (the reference's mma_eligible_ floor,
+ * src/ltx25-metal-ops.cc:342-374) and K % 64 == 0. Host-only. */
+int ltx25_dequant_once_takes(int M, int K, int N);
+
+/* ---- the low-rank adapter delta ------------------------------------------------ */
+
+/* y[M][N] += (x[M][K] . a[rank][K]^T) . b[N][rank]^T, all bf16, in place on
+ * y: r = bf16(x . a^T) with f32 accumulation, then y = bf16(f32(y) + r . b^T)
+ * with the accumulator seeded from y. One fused kernel per 512 adapter
+ * columns; `r` ([M][rank]) and `d` ([M][N]) are the reference signature's
+ * caller scratch and are neither read nor written (either may be NULL).
+ * An empty shape (any of M, K, N, rank <= 0) is a no-op, as in the
+ * reference. Pointers need only bf16 (2-byte) alignment; 16-byte aligned
+ * operands with K % 8 == 0, rank % 8 == 0 and N % 4 == 0 take vector loads.
+ * Replaces MetalOps::lora_add (src/ltx25-metal-ops.h:107-133;
+ * src/ltx25-metal-ops.cc:989-1004) and its matrix-core pair (:940-987). */
+int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
+                   void* y, void* r, void* d, int M, int K, int N, int rank);
+
+/* 1 when ltx25_lora_add runs this shape on the MFMA kernel: every
+ * non-empty shape does (there is no portable fallback on gfx950); 0 for an
+ * empty one. Replaces MetalOps::lora_on_matrix_cores
+ * (src/ltx25-metal-ops.h:134-139). Host-only. */
+int ltx25_lora_on_matrix_cores(int M, int K, int N, int rank);
+
 /* ---- the int8 tier ------------------------------------------------------------ */
 
 /* Turn the int8 tier on (1) or off (0) for ltx25_linear / ltx25_linear_q.

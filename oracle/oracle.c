@@ -8,6 +8,8 @@
  */
 #include "oracle.h"
 
+#include <stdlib.h>
+
 #include <math.h>
 #include <string.h>
 
@@ -279,6 +281,38 @@ void orc_bias_add_bf16(uint16_t* y, const uint16_t* bias, int M, int N)
     const float v = orc_bf16_to_f32(y[i]) + orc_bf16_to_f32(bias[i % N]);
     y[i] = orc_bf16_rne(v);
   }
+}
+
+/* The low-rank adapter delta y += (x . a^T) . b^T, in place on bf16 y,
+ * following MetalOps::lora_add (src/ltx25-metal-ops.cc:989-1004) in its
+ * matrix-core form (:940-987): r = x . a^T is written to a bf16 scratch
+ * (rounded once), and the second product accumulates onto y, seeded from y,
+ * with one rounding to bf16 at the store. a is [rank][K] and b is [N][rank]
+ * (src/ltx25-metal-ops.h:107-117); accumulation here is double. */
+void orc_lora_add(const uint16_t* x, const uint16_t* a, const uint16_t* b,
+                  uint16_t* y, int M, int K, int N, int rank)
+{
+  if (M <= 0 || K <= 0 || N <= 0 || rank <= 0) { return; }
+  float* r = (float*)malloc(sizeof(float) * (size_t)rank);
+  for (int m = 0; m < M; ++m) {
+    const uint16_t* xr = x + (size_t)m * K;
+    for (int j = 0; j < rank; ++j) {
+      const uint16_t* ar = a + (size_t)j * K;
+      double acc = 0.0;
+      for (int k = 0; k < K; ++k) {
+        acc += (double)orc_bf16_to_f32(xr[k]) * (double)orc_bf16_to_f32(ar[k]);
+      }
+      r[j] = orc_bf16_to_f32(orc_bf16_rne((float)acc));
+    }
+    uint16_t* yr = y + (size_t)m * N;
+    for (int n = 0; n < N; ++n) {
+      const uint16_t* br = b + (size_t)n * rank;
+      double acc = (double)orc_bf16_to_f32(yr[n]);
+      for (int j = 0; j < rank; ++j) { acc += (double)r[j] * (double)orc_bf16_to_f32(br[j]); }
+      yr[n] = orc_bf16_rne((float)acc);
+    }
+  }
+  free(r);
 }
 
 /* Per-row symmetric int8: scale = absmax / 127 (f32 division),

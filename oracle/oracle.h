@@ -28,6 +28,11 @@
  *                                    and bit-exact against the reference's
  *                                    stream_ff_ GELU (oracle/_ref)
  *   orc_bias_add_bf16                torch bf16 add of the same operands
+ *   orc_lora_add                     the reference test's own known answer
+ *                                    (f64 over the unrounded draws, rel-L2
+ *                                    < 2e-2), numpy float64 matmuls with the
+ *                                    same bf16 rounding of r, A = 0 leaves y
+ *                                    bit-identical, rank-1 outer product
  *   orc_i8_quantize_rows             numpy rint / absmax closed form
  *   orc_i8_gemm_i32                  numpy int64 matmul
  *   orc_i8_epilogue                  closed form via numpy float32 fma
@@ -72,6 +77,10 @@ void orc_linear_f32_omp(const float* x, const float* w, const float* bias,
                         int M, int K, int N, float* out, int threads);
 void orc_gelu_tanh(const float* in, float* out, size_t n);
 void orc_bias_add_bf16(uint16_t* y, const uint16_t* bias, int M, int N);
+
+/* ---- low-rank adapter delta --------------------------------------------- */
+void orc_lora_add(const uint16_t* x, const uint16_t* a, const uint16_t* b,
+                  uint16_t* y, int M, int K, int N, int rank);
 
 /* ---- int8 tier ---------------------------------------------------------- */
 void orc_i8_quantize_rows(const uint16_t* x_bf16, int M, int K, int8_t* q,

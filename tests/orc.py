@@ -36,6 +36,7 @@ _SIGS = {
     "orc_linear_f32_omp": (None, [_vp, _vp, _vp, _i, _i, _i, _vp, _i]),
     "orc_gelu_tanh": (None, [_vp, _vp, _sz]),
     "orc_bias_add_bf16": (None, [_vp, _vp, _i, _i]),
+    "orc_lora_add": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i]),
     "orc_i8_quantize_rows": (None, [_vp, _i, _i, _vp, _vp]),
     "orc_i8_gemm_i32": (None, [_vp, _vp, _i, _i, _i, _vp]),
     "orc_i8_epilogue": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
@@ -194,6 +195,19 @@ def bias_add_bf16(y, bias) -> np.ndarray:
     bias = _c(bias, np.uint16)
     M, N = y.shape
     lib().orc_bias_add_bf16(_p(y), _p(bias), M, N)
+    return y
+
+
+def lora_add(x_bf16, a_bf16, b_bf16, y_bf16) -> np.ndarray:
+    """y + (x . a^T) . b^T on bf16 bit patterns (uint16); returns the new y."""
+    x = _c(x_bf16, np.uint16)
+    a = _c(a_bf16, np.uint16)
+    b = _c(b_bf16, np.uint16)
+    y = np.array(y_bf16, dtype=np.uint16, copy=True)
+    M, K = x.shape
+    rank = a.shape[0]
+    N = b.shape[0]
+    lib().orc_lora_add(_p(x), _p(a), _p(b), _p(y), M, K, N, rank)
     return y
 
 

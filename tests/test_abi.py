@@ -74,6 +74,32 @@ def test_validation_precedes_any_device_use(pkg, lib):
     assert lib.ltx25_pack_codes(None, fake, fake, 4, 6, 8) == pkg.E_INVAL  # 6 codes != words
 
 
+def test_dequant_once_and_lora_gates(pkg):
+    assert not pkg.dequant_once_takes(8160, 4096, 16384)   # off by default
+    pkg.set_dequant_once(True)
+    try:
+        assert pkg.dequant_once_takes(8160, 4096, 16384)
+        assert not pkg.dequant_once_takes(63, 4096, 4096)     # mma_eligible_'s M floor
+        assert not pkg.dequant_once_takes(64, 4096, 15)       # and its N floor
+        assert not pkg.dequant_once_takes(64, 100, 64)        # K the tile cannot step
+    finally:
+        pkg.set_dequant_once(False)
+    assert pkg.lora_on_matrix_cores(128, 4096, 16384, 32)
+    assert pkg.lora_on_matrix_cores(64, 1024, 1024, 450)
+    assert not pkg.lora_on_matrix_cores(0, 64, 64, 3)
+    assert not pkg.lora_on_matrix_cores(12, 64, 64, 0)
+
+
+def test_lora_validation_precedes_any_device_use(pkg, lib):
+    fake = 0x1000
+    # empty shapes are the reference's no-op (src/ltx25-metal-ops.cc:996): OK, no device use
+    assert lib.ltx25_lora_add(None, fake, fake, fake, fake, None, None, 0, 64, 64, 3) == pkg.OK
+    assert lib.ltx25_lora_add(None, fake, fake, fake, fake, None, None, 12, 64, 64, -1) == pkg.OK
+    assert lib.ltx25_lora_add(None, None, fake, fake, fake, None, None, 12, 64, 64, 3) == pkg.E_INVAL
+    assert lib.ltx25_lora_add(None, fake + 1, fake, fake, fake, None, None, 12, 64, 64,
+                              3) == pkg.E_INVAL
+
+
 def test_i8_takes_gates(pkg):
     pkg.set_i8_gemm(False)
     assert not pkg.i8_takes(8160, 4096, 4096)

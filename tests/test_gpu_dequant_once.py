@@ -1,0 +1,68 @@
+"""The dequant-once A/B arm (ltx25_set_dequant_once) on the GPU.
+
+The reference's M5 route expands the quantized weight into a bf16 scratch and
+runs the dense GEMM over it (src/ltx25-metal-ops.cc:467-502); its test pins
+that the expansion and the fused qmm agree with the dense GEMM over the
+uploaded dequantized weight at rel-L2 0 (tests/ltx25-qlinear-test.cc:
+266-273). Here the expansion is bit-identical to the fused kernel's
+in-register dequant and both arms run the same tile, so the bar is
+bit-identical outputs, with and without bias and the GELU epilogue, and the
+oracle bar on top.
+"""
+import numpy as np
+import pytest
+import torch
+
+import orc
+from gpu_util import dev_bf16, dev_f32, host_bits, make_qweight, rng_normal, say
+
+pytestmark = pytest.mark.gpu
+
+CASES = [  # M, K, N, bits, group, bias, epilogue
+    (320, 4096, 4096, 8, 64, True, 0),     # config 0
+    (256, 1024, 3072, 8, 64, False, 1),    # ff_in shape class, GELU fused
+    (200, 512, 640, 4, 32, True, 0),
+    (64, 2048, 2048, 8, 64, True, 0),      # the arm's M floor
+]
+
+
+@pytest.mark.parametrize("M,K,N,bits,group,has_bias,epi", CASES)
+def test_dequant_once_arm_is_bit_identical_to_fused(pkg, dev, M, K, N, bits, group, has_bias,
+                                                   epi):
+    rng = np.random.default_rng(M * 7 + N)
+    x = orc.bf16_rne(rng_normal(rng, (M, K)))
+    w = rng_normal(rng, (N, K), 0.02)
+    qw, codes, scales, biases, wb = make_qweight(pkg, w, bits, group)
+    bias = rng_normal(rng, (N,), 0.01) if has_bias else None
+    xd = dev_bf16(x)
+    bd = dev_f32(bias) if has_bias else None
+    outs = []
+    try:
+        for arm in (False, True):
+            pkg.set_dequant_once(arm)
+            assert pkg.dequant_once_takes(M, K, N) == arm
+            y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+            say(f"linear_q M={M} K={K} N={N} w{bits}g{group} bias={has_bias} epi={epi} "
+                f"dequant_once={arm}")
+            pkg.linear_q(xd, qw, bd, y, M, K, N, epi)
+            torch.cuda.synchronize()
+            outs.append(host_bits(y))
+    finally:
+        pkg.set_dequant_once(False)
+    assert np.array_equal(outs[0], outs[1])
+    ref = orc.linear_f64(orc.bf16_to_f32(x), orc.bf16_to_f32(wb), bias)
+    if epi == 1:
+        ref = orc.gelu(ref)
+    got = orc.bf16_to_f32(outs[1])
+    assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) <= 1e-2
+
+
+def test_dequant_once_declines_below_the_mma_floor(pkg):
+    pkg.set_dequant_once(True)
+    try:
+        assert not pkg.dequant_once_takes(63, 4096, 4096)
+        assert not pkg.dequant_once_takes(126, 2048, 8)
+        assert pkg.dequant_once_takes(64, 4096, 16)
+    finally:
+        pkg.set_dequant_once(False)
+    assert not pkg.dequant_once_takes(8160, 4096, 16384)

@@ -306,6 +306,71 @@ def test_i8_epilogue_is_one_fma_then_bf16():
         assert checked >= 50
 
 
+# ---- low-rank adapter delta ---------------------------------------------------------------
+# The reference's lora test shapes (tests/ltx25-lora-apply-test.cc:394-409), minus the
+# three large ones, which the GPU tests cover.
+LORA_SMALL = [(12, 64, 64, 3), (8, 32, 64, 3), (12, 64, 32, 3), (12, 64, 4, 3), (12, 64, 256, 5),
+              (6, 64, 64, 1)]
+
+
+def _lora_draws(M, K, N, rank, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    a = (rng.standard_normal((rank, K)) * 0.5).astype(np.float32)
+    b = (rng.standard_normal((N, rank)) * 0.5).astype(np.float32)
+    y = rng.standard_normal((M, N)).astype(np.float32)
+    return x, a, b, y
+
+
+@pytest.mark.parametrize("M,K,N,rank", LORA_SMALL)
+def test_lora_meets_the_reference_tests_f64_bar(M, K, N, rank):
+    # The reference's known answer: y + (x @ A^T) @ B^T in f64 over the UNROUNDED draws,
+    # rel-L2 < 2e-2 (tests/ltx25-lora-apply-test.cc:410-465).
+    x, a, b, y = _lora_draws(M, K, N, rank, 7)
+    want = y.astype(np.float64) + (x.astype(np.float64) @ a.T.astype(np.float64)) @ b.T
+    got = orc.bf16_to_f32(orc.lora_add(orc.bf16_rne(x), orc.bf16_rne(a), orc.bf16_rne(b),
+                                       orc.bf16_rne(y)))
+    assert orc.rel_l2(got, want) < 2e-2
+
+
+@pytest.mark.parametrize("M,K,N,rank", LORA_SMALL + [(33, 96, 40, 17)])
+def test_lora_matches_numpy_with_the_same_roundings(M, K, N, rank):
+    # numpy float64 matmuls: r rounded to bf16 once, then y + r . B^T rounded once.
+    x, a, b, y = (orc.bf16_rne(t) for t in _lora_draws(M, K, N, rank, 11))
+    xf, af, bf, yf = (orc.bf16_to_f32(t).astype(np.float64) for t in (x, a, b, y))
+    r = orc.bf16_to_f32(orc.bf16_rne((xf @ af.T).astype(np.float32))).astype(np.float64)
+    want = orc.bf16_rne((yf + r @ bf.T).astype(np.float32))
+    got = orc.lora_add(x, a, b, y)
+    # double -> float -> bf16 in both; the only freedom is summation order in f64
+    diff = np.abs(orc.bf16_to_f32(got) - orc.bf16_to_f32(want))
+    assert np.count_nonzero(diff) <= max(1, got.size // 1000)
+
+
+def test_lora_zero_a_leaves_y_bit_identical():
+    x, a, b, y = (orc.bf16_rne(t) for t in _lora_draws(16, 64, 48, 4, 3))
+    got = orc.lora_add(x, np.zeros_like(a), b, y)
+    assert np.array_equal(got, y)
+
+
+def test_lora_rank1_is_an_outer_product_and_adds():
+    # rank 1, y = 0: y[m][n] = bf16(bf16(x[m] . a) * b[n]) -- a wrong operand order, a
+    # transposed B or an assignment instead of an add each break one of the two checks.
+    rng = np.random.default_rng(5)
+    M, K, N = 5, 32, 7
+    x = orc.bf16_rne(rng.standard_normal((M, K)).astype(np.float32))
+    a = orc.bf16_rne(rng.standard_normal((1, K)).astype(np.float32))
+    b = orc.bf16_rne(rng.standard_normal((N, 1)).astype(np.float32))
+    r = orc.bf16_to_f32(orc.bf16_rne((orc.bf16_to_f32(x).astype(np.float64) @
+                                      orc.bf16_to_f32(a)[0].astype(np.float64)).astype(np.float32)))
+    want = orc.bf16_rne((r[:, None].astype(np.float64) *
+                         orc.bf16_to_f32(b)[:, 0][None, :].astype(np.float64)).astype(np.float32))
+    zero = np.zeros((M, N), np.uint16)
+    assert np.array_equal(orc.lora_add(x, a, b, zero), want)
+    ones = orc.bf16_rne(np.ones((M, N), np.float32))
+    got = orc.bf16_to_f32(orc.lora_add(x, a, b, ones))
+    assert np.allclose(got, 1.0 + orc.bf16_to_f32(want), rtol=1e-2, atol=1e-2)
+
+
 # ---- committed fixtures -----------------------------------------------------------------
 def test_golden_fixtures_reproduce():
     files = sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz"))

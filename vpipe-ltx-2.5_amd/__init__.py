@@ -70,6 +70,10 @@ SIGNATURES = {
     "ltx25_bias_add": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "ltx25_gelu_tanh": (_i, [_vp, _vp, _vp, _sz]),
     "ltx25_dequant": (_i, [_vp, ctypes.POINTER(QWeightC), _vp, _i, _i]),
+    "ltx25_set_dequant_once": (_i, [_i]),
+    "ltx25_dequant_once_takes": (_i, [_i, _i, _i]),
+    "ltx25_lora_add": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i]),
+    "ltx25_lora_on_matrix_cores": (_i, [_i, _i, _i, _i]),
     "ltx25_set_i8_gemm": (_i, [_i]),
     "ltx25_i8_takes": (_i, [_i, _i, _i]),
     "ltx25_i8_quantize_rows": (_i, [_vp, _vp, _vp, _vp, _i, _i]),
@@ -197,6 +201,25 @@ def unpack_codes(codes, q, N: int, K: int, bits: int, stream=None) -> None:
 
 def f16_to_bf16(src, dst, stream=None) -> None:
     check(load().ltx25_f16_to_bf16(_stream(stream), _ptr(src), _ptr(dst), src.numel()))
+
+
+def set_dequant_once(on: bool) -> None:
+    check(load().ltx25_set_dequant_once(1 if on else 0))
+
+
+def dequant_once_takes(M: int, K: int, N: int) -> bool:
+    return bool(load().ltx25_dequant_once_takes(M, K, N))
+
+
+def lora_add(x, a, b, y, M: int, K: int, N: int, rank: int, r=None, d=None,
+             stream=None) -> None:
+    """y += (x . a^T) . b^T in place (MetalOps::lora_add); r and d are unused scratch."""
+    check(load().ltx25_lora_add(_stream(stream), _ptr(x), _ptr(a), _ptr(b), _ptr(y), _ptr(r),
+                                _ptr(d), M, K, N, rank))
+
+
+def lora_on_matrix_cores(M: int, K: int, N: int, rank: int) -> bool:
+    return bool(load().ltx25_lora_on_matrix_cores(M, K, N, rank))
 
 
 def set_i8_gemm(on: bool) -> None:

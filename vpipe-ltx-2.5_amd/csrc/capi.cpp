@@ -52,11 +52,14 @@ struct DeviceState {
   size_t cnt_bytes = 0;
   void* i8 = nullptr;        // int8 tier operands: xq | sx | wq | sw
   size_t i8_bytes = 0;
+  void* deq = nullptr;       // dequant-once arm: bf16 [N][K] expansion
+  size_t deq_bytes = 0;
 };
 
 std::mutex g_mu;
 DeviceState g_dev[kMaxDevices];
 int g_i8_on = 0;
+int g_deq_once = 0;
 
 // Check (once per device) that the current device is gfx950.
 int current_device(DeviceState** out)
@@ -215,6 +218,23 @@ int run_linear(hipStream_t st, const void* x, const ltx25_qweight* w,
   d.qbias = (const uint16_t*)w->qbias;
   d.bits = w->quantized ? w->bits : 16;
   d.group = w->quantized ? w->group : 64;
+  if (w->quantized && ltx25_dequant_once_takes(M, K, N)) {
+    // The dequant-once arm: expand W into the grow-only bf16 scratch, then
+    // the same GEMM tile over the dense copy. The expansion is bit-identical
+    // to the in-register dequant, so both arms produce the same bits.
+    std::lock_guard<std::mutex> lk(g_mu);
+    rc = grow(&ds->deq, &ds->deq_bytes, (size_t)N * K * 2);
+    if (rc != LTX25_OK) { return rc; }
+    const hipError_t e = ltx25::launch_dequant(w->codes, (const uint16_t*)w->scales,
+                                               (const uint16_t*)w->qbias, w->bits,
+                                               w->group, (uint16_t*)ds->deq, N, K, st);
+    if (e != hipSuccess) { return hip_fail(e, "dequant-once launch"); }
+    d.w = ds->deq;
+    d.scales = nullptr;
+    d.qbias = nullptr;
+    d.bits = 16;
+    d.group = 64;
+  }
   d.bias = bias;
   d.bias_type = bias != nullptr ? bias_dtype : ltx25::kBiasNone;
   d.epilogue = epilogue;
@@ -391,6 +411,53 @@ int ltx25_dequant(void* stream, const ltx25_qweight* w, void* out_bf16, int N,
                                              w->group, (uint16_t*)out_bf16, N, K,
                                              (hipStream_t)stream);
   return e == hipSuccess ? LTX25_OK : hip_fail(e, "dequant launch");
+}
+
+int ltx25_set_dequant_once(int on)
+{
+  g_deq_once = on != 0;
+  return LTX25_OK;
+}
+
+int ltx25_dequant_once_takes(int M, int K, int N)
+{
+  return g_deq_once && M >= 64 && N >= 16 && K > 0 && K % 64 == 0 ? 1 : 0;
+}
+
+int ltx25_lora_on_matrix_cores(int M, int K, int N, int rank)
+{
+  return M > 0 && K > 0 && N > 0 && rank > 0 ? 1 : 0;
+}
+
+int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
+                   void* y, void* r, void* d, int M, int K, int N, int rank)
+{
+  (void)r;
+  (void)d;
+  // The reference returns without encoding anything for an empty shape
+  // (src/ltx25-metal-ops.cc:996).
+  if (M <= 0 || K <= 0 || N <= 0 || rank <= 0) { return LTX25_OK; }
+  if (x == nullptr || a == nullptr || b == nullptr || y == nullptr) {
+    return fail(LTX25_E_INVAL, "x, a, b or y is null");
+  }
+  if ((((uintptr_t)x | (uintptr_t)a | (uintptr_t)b | (uintptr_t)y) & 1u) != 0) {
+    return fail(LTX25_E_INVAL, "a bf16 tensor is not 2-byte aligned");
+  }
+  DeviceState* ds = nullptr;
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const bool vec = K % 8 == 0 && rank % 8 == 0 && N % 4 == 0 && aligned16(x) &&
+                   aligned16(a) && aligned16(b) && ((uintptr_t)y & 7u) == 0;
+  const uint16_t* pa = (const uint16_t*)a;
+  const uint16_t* pb = (const uint16_t*)b;
+  for (int c = 0; c < rank; c += ltx25::kLoraMaxRank) {
+    const int rp = rank - c < ltx25::kLoraMaxRank ? rank - c : ltx25::kLoraMaxRank;
+    const hipError_t e = ltx25::launch_lora((const uint16_t*)x, pa + (size_t)c * K, pb + c,
+                                            (uint16_t*)y, M, K, N, rp, rank, vec,
+                                            ds->cu_count, (hipStream_t)stream);
+    if (e != hipSuccess) { return hip_fail(e, "lora launch"); }
+  }
+  return LTX25_OK;
 }
 
 int ltx25_set_i8_gemm(int on)

@@ -103,6 +103,17 @@ SkinnyPlan plan_skinny(int M, int N, int K, int cu_count);
 hipError_t launch_skinny(const GemmDesc& d, const SkinnyPlan& plan, float* partial,
                          int* counters, hipStream_t stream);
 
+// The low-rank adapter delta y += (x . A^T) . B^T (lora.hip). One launch
+// covers at most kLoraMaxRank adapter columns: `a` points at the pass's
+// first row of A [rank][K], `b` at its first column of B [N][ldb]. `vec`
+// selects 16-byte operand loads (K % 8 == 0, ldb % 8 == 0, N % 4 == 0 and
+// aligned pointers).
+constexpr int kLoraMaxRank = 512;
+int lora_splits(int M, int N, int cu_count);
+hipError_t launch_lora(const uint16_t* x, const uint16_t* a, const uint16_t* b,
+                       uint16_t* y, int M, int K, int N, int rank, int ldb,
+                       bool vec, int cu_count, hipStream_t stream);
+
 hipError_t launch_bias_add(uint16_t* y, const void* bias, int bias_type,
                            int M, int N, hipStream_t stream);
 hipError_t launch_gelu(const uint16_t* x, uint16_t* y, size_t n,

@@ -95,6 +95,22 @@ public:
     note(ltx25_gelu_tanh(enc, x, y, (size_t)n));
   }
 
+  // y[M][N] += (x . a^T) . b^T (src/ltx25-metal-ops.h:107-133). `r` and `d`
+  // keep the reference signature's caller scratch; the fused kernel uses
+  // neither.
+  void lora_add(hipStream_t enc, const void* x, const void* a, const void* b, void* y,
+                void* r, void* d, int M, int K, int N, int rank) const
+  {
+    note(ltx25_lora_add(enc, x, a, b, y, r, d, M, K, N, rank));
+  }
+  bool lora_on_matrix_cores(int M, int K, int N, int rank) const noexcept
+  {
+    return ltx25_lora_on_matrix_cores(M, K, N, rank) != 0;
+  }
+
+  // The dequant-once A/B arm (src/ltx25-metal-ops.cc:467-502).
+  void set_dequant_once(bool on) { ltx25_set_dequant_once(on ? 1 : 0); }
+
   // src/ltx25-metal-ops.h:151,157.
   void set_i8_gemm(bool on) { ltx25_set_i8_gemm(on ? 1 : 0); }
   bool i8_takes(int M, int K, int N) const noexcept { return ltx25_i8_takes(M, K, N) != 0; }
