@@ -242,6 +242,55 @@ int ltx25_f16_to_bf16(void* stream, const void* in_f16, void* out_bf16,
 int ltx25_qweight_infer(int K, long scales_cols, long codes_cols, int* bits,
                         int* group);
 
+/* ---- the on-disk pack reader ------------------------------------------------------ */
+
+/* An open .safetensors file: mapped read-only, header parsed on the host.
+ * The device buffers it binds belong to it until ltx25_pack_close. */
+typedef struct ltx25_pack ltx25_pack;
+
+/* Open and parse a pack. No device work. Replaces the weight-set reads of
+ * the reference's loader (src/ltx25-dit-weights.cc:170-190), which go
+ * through vpipe's WeightSet. */
+int ltx25_pack_open(const char* path, ltx25_pack** out);
+
+/* Drain the device, free every buffer the pack bound, unmap, close. */
+void ltx25_pack_close(ltx25_pack* pack);
+
+/* A tensor's safetensors dtype ("U32", "F16", "BF16", "F32", ...), rank
+ * and dims (up to 8). Host-only. LTX25_E_INVAL when the name is absent. */
+int ltx25_pack_tensor(const ltx25_pack* pack, const char* name, char dtype[16],
+                      int* ndim, long dims[8]);
+
+/* A string from the header's __metadata__, or NULL. */
+const char* ltx25_pack_metadata(const ltx25_pack* pack, const char* key);
+
+/* A tensor as bf16 in device memory the pack owns: BF16 as stored, F16
+ * converted on the device, F32 converted on the host, both with round to
+ * nearest even; cached per name. Replaces get_as_bf16_
+ * (src/ltx25-dit-weights.cc:230-278). */
+int ltx25_pack_read_bf16(ltx25_pack* pack, void* stream, const char* name,
+                         const void** dev_bf16, size_t* count);
+
+/* Bind one linear that may be quantized. When NAME.scales and NAME.weight
+ * are both 2-D (and K > 0) it is quantized: bits and group come from the
+ * shapes (ltx25_qweight_infer), `*group` is set by the first quantized
+ * linear and checked on every later one, the u32 codes are uploaded
+ * untouched and NAME.scales / NAME.biases are read as bf16. Otherwise
+ * NAME.weight is the dense weight, read as bf16. A missing tensor is named
+ * in `miss` (when non-NULL and still empty). The result's pointers are
+ * owned by the pack. Replaces need_q_ (src/ltx25-dit-weights.cc:352-403;
+ * the bind entry point bind_qlinear, src/ltx25-dit-weights.h:170-175). */
+int ltx25_pack_bind_qlinear(ltx25_pack* pack, void* stream, const char* name,
+                            int K, int* group, ltx25_qweight* out, char* miss,
+                            size_t miss_len);
+
+/* 1 when the DiT quantizer packs this tensor: inside a block stack (name
+ * contains "_blocks."), a 2-D float ".weight", not a norm or embedding,
+ * and not one of the two 2-D floats that are not matrices ("scale_shift"
+ * tables, the "to_gate_logits" per-head gate). Host-only. Restates the
+ * selection of src/ltx25-quant-family.cc:44-71. */
+int ltx25_pack_quantizable(const char* name, const char* dtype, int ndim);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,6 +84,16 @@ SIGNATURES = {
     "ltx25_quantize_affine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i]),
     "ltx25_f16_to_bf16": (_i, [_vp, _vp, _vp, _sz]),
     "ltx25_qweight_infer": (_i, [_i, _long, _long, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
+    "ltx25_pack_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "ltx25_pack_close": (None, [_vp]),
+    "ltx25_pack_tensor": (_i, [_vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_i),
+                               ctypes.POINTER(_long)]),
+    "ltx25_pack_metadata": (ctypes.c_char_p, [_vp, ctypes.c_char_p]),
+    "ltx25_pack_read_bf16": (_i, [_vp, _vp, ctypes.c_char_p, ctypes.POINTER(_vp),
+                                  ctypes.POINTER(_sz)]),
+    "ltx25_pack_bind_qlinear": (_i, [_vp, _vp, ctypes.c_char_p, _i, ctypes.POINTER(_i),
+                                     ctypes.POINTER(QWeightC), ctypes.c_char_p, _sz]),
+    "ltx25_pack_quantizable": (_i, [ctypes.c_char_p, ctypes.c_char_p, _i]),
 }
 
 _lib = None
@@ -251,3 +261,78 @@ def qweight_infer(K: int, scales_cols: int, codes_cols: int, group: int = 0) -> 
     g = ctypes.c_int(group)
     check(load().ltx25_qweight_infer(K, scales_cols, codes_cols, ctypes.byref(b), ctypes.byref(g)))
     return b.value, g.value
+
+
+def _pack_stream(stream):
+    """torch's current stream when a device is visible; NULL otherwise, so
+    that host-side validation runs (and fails) without touching a device."""
+    if stream is not None:
+        return stream
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream if torch.cuda.is_available() else None
+
+
+class Pack:
+    """An open .safetensors pack (ltx25_pack_*). Device tensors it binds stay
+    valid until close()."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        check(load().ltx25_pack_open(path.encode(), ctypes.byref(h)))
+        self._h = h
+        self.group = 0   # the checkpoint's group, set by the first quantized bind
+
+    def close(self) -> None:
+        if self._h:
+            load().ltx25_pack_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def tensor(self, name: str) -> tuple[str, tuple[int, ...]]:
+        dt = ctypes.create_string_buffer(16)
+        nd = ctypes.c_int(0)
+        dims = (ctypes.c_long * 8)()
+        check(load().ltx25_pack_tensor(self._h, name.encode(), dt, ctypes.byref(nd), dims))
+        return dt.value.decode(), tuple(dims[i] for i in range(nd.value))
+
+    def metadata(self, key: str):
+        v = load().ltx25_pack_metadata(self._h, key.encode())
+        return None if v is None else v.decode()
+
+    def read_bf16(self, name: str, stream=None) -> tuple[int, int]:
+        """(device pointer, element count) of the tensor as bf16."""
+        p = ctypes.c_void_p()
+        n = ctypes.c_size_t(0)
+        check(load().ltx25_pack_read_bf16(self._h, _pack_stream(stream), name.encode(),
+                                          ctypes.byref(p), ctypes.byref(n)))
+        return p.value, n.value
+
+    def bind_qlinear(self, name: str, K: int, stream=None) -> QWeightC:
+        """The C weight descriptor of linear `name` (quantized or dense)."""
+        out = QWeightC()
+        g = ctypes.c_int(self.group)
+        miss = ctypes.create_string_buffer(256)
+        rc = load().ltx25_pack_bind_qlinear(self._h, _pack_stream(stream), name.encode(), K,
+                                            ctypes.byref(g), ctypes.byref(out), miss, 256)
+        if rc != OK:
+            raise Ltx25Error(rc, last_error() + (f" (missing {miss.value.decode()})"
+                                                 if miss.value else ""))
+        self.group = g.value
+        return out
+
+
+def pack_quantizable(name: str, dtype: str, ndim: int) -> bool:
+    return bool(load().ltx25_pack_quantizable(name.encode(), dtype.encode(), ndim))
+
+
+def linear_qc(x, cw: QWeightC, bias, y, M: int, K: int, N: int, epilogue: int = EPI_NONE,
+              stream=None) -> None:
+    """linear over an already-built C weight descriptor (e.g. from Pack.bind_qlinear)."""
+    check(load().ltx25_linear_q_ex(_stream(stream), _ptr(x), ctypes.byref(cw), _ptr(bias),
+                                   bias_dtype_of(bias), _ptr(y), M, K, N, epilogue))

@@ -33,6 +33,25 @@ int fail(int code, const char* fmt, ...)
   return code;
 }
 
+}  // namespace
+
+namespace ltx25 {
+
+int set_error(int code, const char* fmt, ...)
+{
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+}  // namespace ltx25
+
+namespace {
+
 int hip_fail(hipError_t e, const char* what)
 {
   return fail(LTX25_E_HIP, "%s: %s", what, hipGetErrorString(e));

@@ -53,6 +53,10 @@ __device__ __forceinline__ float gelu_tanh(float x)
 
 // ---- internal launcher interface ------------------------------------------
 
+// Record `code` and a printf-style message as this thread's last error
+// (what ltx25_last_error returns); returns `code`.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
 // Element type of a bias vector (matches LTX25_DT_* in the C header).
 enum BiasType : int { kBiasNone = 0, kBiasBf16 = 1, kBiasF32 = 2 };
 enum Epilogue : int { kEpiNone = 0, kEpiGelu = 1 };
