@@ -16,9 +16,11 @@ Also reported on the same line:
   c4        config 4: the 28 linears of one joint audio-video block (22
             launches with the fused QKV / KV packs) over 48 blocks of
             distinct weights, seconds of linear time per denoise step
-  roofline  the dominant kernel (the 256x256 w8 GEMM serving both FFN
-            GEMMs): algorithmic FLOP per launch / its mean launch time,
-            from HIP events on the launch stream
+  roofline  the dominant kernel: at M = 8160 linear_q's default route is the
+            dequant-once arm (a 33 us weight expansion, then the dense
+            256x256 GEMM), so the GEMM kernel -- timed on its own with HIP
+            events on the launch stream, over the expanded weights --
+            gives algorithmic FLOP per launch / mean launch time
   cpu_baseline  the reference's CPU linear (oracle/_ref, built from the
             reference's sources) timed on this host, 1 thread, on a row
             sample of the up-projection
@@ -104,6 +106,11 @@ class EventTimer:
 
 # ---- config 2: the FFN pair (headline) -------------------------------------------------
 def bench_ffn(pkg, torch, steps, warmup):
+    """The pair through ltx25_linear_q with the library's default routing
+    (the dequant-once arm at M = 8160: weight expansion + dense GEMM, both
+    inside each timed call). The roofline kernel -- the dense GEMM the route
+    runs -- is also timed on its own, on the same stream, over the expanded
+    weights: that is the launch the roofline's `achieved` divides by."""
     M, D, H = 8160, 4096, 16384
     g = torch.Generator(device="cuda")
     g.manual_seed(2)
@@ -112,6 +119,7 @@ def bench_ffn(pkg, torch, steps, warmup):
     w2 = make_qweight(pkg, torch, D, H, g)
     h = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
     y = torch.empty((M, D), dtype=torch.bfloat16, device="cuda")
+    route = "dequant-once + dense GEMM" if pkg.dequant_once_takes(M, D, H) else "fused"
 
     def up():
         pkg.linear_q(x, w1, None, h, M, D, H, pkg.EPI_GELU_TANH)
@@ -132,16 +140,41 @@ def bench_ffn(pkg, torch, steps, warmup):
     wall = time.perf_counter() - t0
     flop = 2.0 * M * D * H
     up_ms, down_ms = timer.mean_ms("up"), timer.mean_ms("down")
-    return {
+    out = {
+        "route": route,
         "ms_per_step": wall / steps * 1e3,
         "tflops": 2 * flop / (wall / steps) / 1e12,
         "up_ms": up_ms,
         "down_ms": down_ms,
         "up_tflops": flop / (up_ms * 1e-3) / 1e12,
         "down_tflops": flop / (down_ms * 1e-3) / 1e12,
-        "kernel_mean_ms": (up_ms + down_ms) / 2,
         "flop_per_launch": flop,
     }
+    if route == "fused":
+        out["kernel_mean_ms"] = (up_ms + down_ms) / 2
+        return out
+    # the route's two kernels, each on its own
+    d1 = torch.empty((H, D), dtype=torch.bfloat16, device="cuda")
+    d2 = torch.empty((D, H), dtype=torch.bfloat16, device="cuda")
+    c1, c2 = pkg.dense_weight(d1), pkg.dense_weight(d2)
+    kt = EventTimer(torch)
+    for i in range(warmup + steps):
+        t = kt if i >= warmup else EventTimer(torch)
+        t.record("deq_up", lambda: pkg.dequant(w1, d1, H, D))
+        t.record("gemm_up", lambda: pkg.linear_qc(x, c1, None, h, M, D, H, pkg.EPI_GELU_TANH))
+        t.record("deq_down", lambda: pkg.dequant(w2, d2, D, H))
+        t.record("gemm_down", lambda: pkg.linear_qc(h, c2, None, y, M, H, D))
+    torch.cuda.synchronize()
+    deq_bytes = H * D * (1 + 2) + (H * D // 64) * 4
+    out.update({
+        "gemm_up_ms": kt.mean_ms("gemm_up"),
+        "gemm_down_ms": kt.mean_ms("gemm_down"),
+        "dequant_us": (kt.mean_ms("deq_up") + kt.mean_ms("deq_down")) / 2 * 1e3,
+        "dequant_GBps": deq_bytes / ((kt.mean_ms("deq_up") + kt.mean_ms("deq_down")) / 2 * 1e-3)
+        / 1e9,
+        "kernel_mean_ms": (kt.mean_ms("gemm_up") + kt.mean_ms("gemm_down")) / 2,
+    })
+    return out
 
 
 # ---- config 1: audio skinny GEMMs -------------------------------------------------------
@@ -256,7 +289,7 @@ def bench_dequant_once(pkg, torch, steps, warmup):
             res["dequant_once" if arm else "fused"] = {
                 "ms": ms, "TFLOPs": 2.0 * M * D * H / (ms * 1e-3) / 1e12}
     finally:
-        pkg.set_dequant_once(False)
+        pkg.set_dequant_once(pkg.DEQUANT_ONCE_AUTO)
     return res
 
 
@@ -355,7 +388,7 @@ def bench_c4(pkg, torch, steps, warmup, blocks=48):
 
 
 # ---- CPU baseline -------------------------------------------------------------------------
-def cpu_baseline(rows=64):
+def cpu_baseline(rows=384):
     """The reference's CPU linear (oracle/_ref: src/ltx25-block-ref.cc:11-28
     compiled from the reference sources) on `rows` rows of the up-projection,
     over the weight dequantized by the oracle's restatement of the
@@ -451,7 +484,8 @@ def pmc_summary(fetch_csv, write_csv, cmd):
     w_fac = COPY_BYTES / (wr[cal][2] * 1024)
     groups = {}
     for i, (name, grid, v) in fe.items():
-        if "qgemm_kernel" not in name and "splitk_reduce" not in name:
+        if ("qgemm_kernel" not in name and "splitk_reduce" not in name and
+                "dequant_kernel" not in name):
             continue
         short = name[name.index("ltx25::"):].split("(ltx25")[0].replace("(anonymous namespace)::", "")
         g = groups.setdefault((short, grid), [0, 0.0, 0.0])
@@ -459,10 +493,14 @@ def pmc_summary(fetch_csv, write_csv, cmd):
         g[1] += v * 1024 * f_fac
         g[2] += wr.get(i, ("", 0, 0.0))[2] * 1024 * w_fac
     M, D, H = 8160, 4096, 16384
-    alg = {  # read, write bytes of the two FFN GEMMs
-        "up": (M * D * 2 + H * D + H * D // 64 * 4, M * H * 2),
-        "down": (M * H * 2 + D * H + D * H // 64 * 4, M * D * 2),
-    }
+
+    def alg(which, dense):
+        """read, write bytes of an FFN GEMM: w8g64 codes + scales/biases, or the bf16
+        expansion the dequant-once route's dense GEMM reads."""
+        k, n = (D, H) if which == "up" else (H, D)
+        w = n * k * 2 if dense else n * k + n * k // 64 * 4
+        return (M * k * 2 + w, M * n * 2)
+
     mt = (M + 255) // 256
     ffn_grid = {mt * (H // 256) * 512: "up", mt * (D // 256) * 512: "down"}
     lines = ["# HBM traffic per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE)", "",
@@ -476,12 +514,17 @@ def pmc_summary(fetch_csv, write_csv, cmd):
     ffn = []
     for (short, grid), (n, fb, wb) in sorted(groups.items(), key=lambda kv: -kv[1][1] / kv[1][0]):
         which = ffn_grid.get(grid) if "256, 256" in short else None
-        a = f"{alg[which][0] / 1e6:.1f} / {alg[which][1] / 1e6:.1f} ({which})" if which else ""
+        dense = ", 16, " in short
+        a = (f"{alg(which, dense)[0] / 1e6:.1f} / {alg(which, dense)[1] / 1e6:.1f} ({which})"
+             if which else "")
         lines.append(f"| `{short}` | {grid} | {n} | {fb / n / 1e6:.1f} | {wb / n / 1e6:.1f} | {a} |")
         if which:
-            ffn.append(((fb + wb) / n, which))
-    traffic = sum(t for t, _ in ffn) / len(ffn) if ffn else None
-    alg_mean = sum(sum(alg[w]) for _, w in ffn) / len(ffn) if ffn else None
+            ffn.append(((fb + wb) / n, which, dense))
+    # the roofline kernel: the dense GEMM when the route ran it, else the fused one
+    if any(d for _, _, d in ffn):
+        ffn = [f for f in ffn if f[2]]
+    traffic = sum(t for t, _, _ in ffn) / len(ffn) if ffn else None
+    alg_mean = sum(sum(alg(w, d)) for _, w, d in ffn) / len(ffn) if ffn else None
     lines += ["", f"FFN GEMM (the roofline kernel, mean of up and down): "
               f"{traffic / 1e6:.1f} MB per launch against {alg_mean / 1e6:.1f} MB algorithmic."
               if traffic else "", ""]
@@ -492,6 +535,32 @@ def pmc_summary(fetch_csv, write_csv, cmd):
                    "algorithmic_bytes": round(alg_mean) if alg_mean else None,
                    "fetch_factor": round(f_fac, 4), "write_factor": round(w_fac, 4),
                    "source": "profiles/qgemm_ffn_hbm_traffic.md"}, f, indent=1)
+    print("\n".join(lines))
+
+
+def kernel_summary(db, out, cmd, note):
+    """rocprofv3 kernel-trace database -> a short markdown table (via rocpd2summary)."""
+    import csv
+    import subprocess
+    import tempfile
+
+    d = tempfile.mkdtemp()
+    subprocess.run(["rocpd2summary", "-i", os.path.abspath(db), "-f", "csv", "-d", d, "-o", "k"],
+                   cwd="/tmp", check=True, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
+    with open(os.path.join(d, "k_kernels_summary.csv")) as f:
+        rows = list(csv.DictReader(f))
+    lines = [f"# Kernel stats: {note}", "", "Commands (MI355X box, repo root):", "", "```", cmd,
+             f"python3 bench.py --kernel-summary <out>/run_results.db {out} '<cmd>' '<note>'",
+             "```", "", "| kernel | calls | avg us | min us | max us | total % |",
+             "|---|---|---|---|---|---|"]
+    for r in rows:
+        n = r["Name"]
+        n = n if len(n) <= 100 else n[:100] + "..."
+        lines.append(f"| `{n}` | {r['Calls']} | {float(r['Average (Nsec)']) / 1e3:.1f} | "
+                     f"{float(r['Min (Nsec)']) / 1e3:.1f} | {float(r['Max (Nsec)']) / 1e3:.1f} | "
+                     f"{float(r['Percent (Inc)']):.1f} |")
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
 
 
@@ -511,7 +580,12 @@ def main():
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "CMD"),
                     help="summarise two rocprofv3 --pmc counter files into profiles/ and exit")
+    ap.add_argument("--kernel-summary", nargs=4, metavar=("DB", "OUT_MD", "CMD", "NOTE"),
+                    help="summarise a rocprofv3 --kernel-trace database into OUT_MD and exit")
     args = ap.parse_args()
+    if args.kernel_summary:
+        kernel_summary(*args.kernel_summary)
+        return
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
         return
@@ -594,7 +668,9 @@ def main():
         "pct_bf16_peak": round(100 * ffn["tflops"] / PEAK_BF16_TFLOPS, 2),
         "ffn": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in ffn.items()},
         "roofline": {
-            "kernel": "qgemm_kernel<256,256,2,4,8,false> (up with GELU and down)",
+            "kernel": ("qgemm_kernel<256,256,2,4,16,false> (dense GEMM of the dequant-once route; "
+                       "up with GELU and down)" if ffn["route"] != "fused" else
+                       "qgemm_kernel<256,256,2,4,8,false> (up with GELU and down)"),
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,

@@ -136,19 +136,30 @@ int ltx25_gelu_tanh(void* stream, const void* x, void* y, size_t n);
 int ltx25_dequant(void* stream, const ltx25_qweight* w, void* out_bf16,
                   int N, int K);
 
-/* Route quantized linears through the dequant-once arm (1) or the fused
- * dequant-in-GEMM kernel (0, the default). The arm expands W into a
- * grow-only bf16 [N][K] scratch shared across calls (the reference's
- * `_w_deq`, src/ltx25-metal-ops.h:843-845) and runs the dense GEMM over it;
- * the expansion equals the fused kernel's in-register dequant, so both arms
- * return the same bits and differ only in speed and in 2 B per weight of
- * extra traffic. Replaces the reference's dequant_mma_ route
- * (src/ltx25-metal-ops.cc:467-502, tried first at :544) as an A/B hook. */
-int ltx25_set_dequant_once(int on);
+/* The dequant-once arm: expand W into a grow-only bf16 [N][K] scratch shared
+ * across calls (the reference's `_w_deq`, src/ltx25-metal-ops.h:843-845),
+ * then run the dense GEMM over it. The expansion equals the fused kernel's
+ * in-register dequant, so both routes return the same bits; they differ in
+ * speed and in 2 B per weight of extra traffic. The fused kernel
+ * dequantizes each weight once per 256-row tile, so the arm wins on tall
+ * GEMMs: measured on MI355X at the DiT's widths it is 3-17% faster from
+ * M = 4096 up and slower below M = 2048.
+ *   OFF   always the fused dequant-in-GEMM kernel
+ *   ON    the arm whenever the dense tile takes the shape (M >= 64,
+ *         N >= 16: the reference's mma_eligible_ floor,
+ *         src/ltx25-metal-ops.cc:342-374)
+ *   AUTO  (the default) the arm from M >= LTX25_DEQUANT_ONCE_AUTO_MIN_M
+ * The reference takes its dequant_mma_ route first whenever it is eligible
+ * (src/ltx25-metal-ops.cc:467-502, tried at :544); AUTO keeps that route
+ * where it is the faster one on this hardware. */
+#define LTX25_DEQUANT_ONCE_OFF 0
+#define LTX25_DEQUANT_ONCE_ON 1
+#define LTX25_DEQUANT_ONCE_AUTO 2
+#define LTX25_DEQUANT_ONCE_AUTO_MIN_M 4096
+int ltx25_set_dequant_once(int mode);
 
-/* 1 when ltx25_linear_q would take the dequant-once arm for this shape:
- * the arm is on, M >= 64 and N >= 16 (the reference's mma_eligible_ floor,
- * src/ltx25-metal-ops.cc:342-374) and K % 64 == 0. Host-only. */
+/* 1 when ltx25_linear_q would take the dequant-once arm for this shape
+ * under the current mode (K must also be a multiple of 64). Host-only. */
 int ltx25_dequant_once_takes(int M, int K, int N);
 
 /* ---- the low-rank adapter delta ------------------------------------------------ */

@@ -74,16 +74,23 @@ def test_validation_precedes_any_device_use(pkg, lib):
     assert lib.ltx25_pack_codes(None, fake, fake, 4, 6, 8) == pkg.E_INVAL  # 6 codes != words
 
 
-def test_dequant_once_and_lora_gates(pkg):
-    assert not pkg.dequant_once_takes(8160, 4096, 16384)   # off by default
-    pkg.set_dequant_once(True)
+def test_dequant_once_and_lora_gates(pkg, lib):
+    # AUTO by default: the arm for tall GEMMs only
+    assert pkg.dequant_once_takes(8160, 4096, 16384)
+    assert pkg.dequant_once_takes(4096, 2048, 8192)
+    assert not pkg.dequant_once_takes(4095, 4096, 4096)
+    assert not pkg.dequant_once_takes(126, 2048, 6144)
     try:
-        assert pkg.dequant_once_takes(8160, 4096, 16384)
+        pkg.set_dequant_once(pkg.DEQUANT_ONCE_OFF)
+        assert not pkg.dequant_once_takes(8160, 4096, 16384)
+        pkg.set_dequant_once(pkg.DEQUANT_ONCE_ON)
+        assert pkg.dequant_once_takes(320, 4096, 4096)
         assert not pkg.dequant_once_takes(63, 4096, 4096)     # mma_eligible_'s M floor
         assert not pkg.dequant_once_takes(64, 4096, 15)       # and its N floor
         assert not pkg.dequant_once_takes(64, 100, 64)        # K the tile cannot step
+        assert lib.ltx25_set_dequant_once(7) == pkg.E_INVAL
     finally:
-        pkg.set_dequant_once(False)
+        pkg.set_dequant_once(pkg.DEQUANT_ONCE_AUTO)
     assert pkg.lora_on_matrix_cores(128, 4096, 16384, 32)
     assert pkg.lora_on_matrix_cores(64, 1024, 1024, 450)
     assert not pkg.lora_on_matrix_cores(0, 64, 64, 3)

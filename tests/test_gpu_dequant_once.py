@@ -48,7 +48,7 @@ def test_dequant_once_arm_is_bit_identical_to_fused(pkg, dev, M, K, N, bits, gro
             torch.cuda.synchronize()
             outs.append(host_bits(y))
     finally:
-        pkg.set_dequant_once(False)
+        pkg.set_dequant_once(pkg.DEQUANT_ONCE_AUTO)
     assert np.array_equal(outs[0], outs[1])
     ref = orc.linear_f64(orc.bf16_to_f32(x), orc.bf16_to_f32(wb), bias)
     if epi == 1:
@@ -64,5 +64,6 @@ def test_dequant_once_declines_below_the_mma_floor(pkg):
         assert not pkg.dequant_once_takes(126, 2048, 8)
         assert pkg.dequant_once_takes(64, 4096, 16)
     finally:
-        pkg.set_dequant_once(False)
-    assert not pkg.dequant_once_takes(8160, 4096, 16384)
+        pkg.set_dequant_once(pkg.DEQUANT_ONCE_AUTO)
+    assert pkg.dequant_once_takes(8160, 4096, 16384)   # AUTO: tall shapes
+    assert not pkg.dequant_once_takes(320, 4096, 4096)

@@ -33,6 +33,10 @@ DT_F32 = 2
 EPI_NONE = 0
 EPI_GELU_TANH = 1
 
+DEQUANT_ONCE_OFF = 0
+DEQUANT_ONCE_ON = 1
+DEQUANT_ONCE_AUTO = 2
+
 
 class QWeightC(ctypes.Structure):
     """ltx25_qweight (mirrors QWeight, src/ltx25-metal-ops.h:45-57)."""
@@ -213,8 +217,9 @@ def f16_to_bf16(src, dst, stream=None) -> None:
     check(load().ltx25_f16_to_bf16(_stream(stream), _ptr(src), _ptr(dst), src.numel()))
 
 
-def set_dequant_once(on: bool) -> None:
-    check(load().ltx25_set_dequant_once(1 if on else 0))
+def set_dequant_once(mode) -> None:
+    """DEQUANT_ONCE_OFF / _ON / _AUTO (the default); a bool means OFF / ON."""
+    check(load().ltx25_set_dequant_once(int(mode)))
 
 
 def dequant_once_takes(M: int, K: int, N: int) -> bool:

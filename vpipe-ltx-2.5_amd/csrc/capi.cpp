@@ -78,7 +78,7 @@ struct DeviceState {
 std::mutex g_mu;
 DeviceState g_dev[kMaxDevices];
 int g_i8_on = 0;
-int g_deq_once = 0;
+int g_deq_once = LTX25_DEQUANT_ONCE_AUTO;
 
 // Check (once per device) that the current device is gfx950.
 int current_device(DeviceState** out)
@@ -432,15 +432,21 @@ int ltx25_dequant(void* stream, const ltx25_qweight* w, void* out_bf16, int N,
   return e == hipSuccess ? LTX25_OK : hip_fail(e, "dequant launch");
 }
 
-int ltx25_set_dequant_once(int on)
+int ltx25_set_dequant_once(int mode)
 {
-  g_deq_once = on != 0;
+  if (mode != LTX25_DEQUANT_ONCE_OFF && mode != LTX25_DEQUANT_ONCE_ON &&
+      mode != LTX25_DEQUANT_ONCE_AUTO) {
+    return fail(LTX25_E_INVAL, "dequant-once mode %d is not OFF, ON or AUTO", mode);
+  }
+  g_deq_once = mode;
   return LTX25_OK;
 }
 
 int ltx25_dequant_once_takes(int M, int K, int N)
 {
-  return g_deq_once && M >= 64 && N >= 16 && K > 0 && K % 64 == 0 ? 1 : 0;
+  if (g_deq_once == LTX25_DEQUANT_ONCE_OFF) { return 0; }
+  if (M < 64 || N < 16 || K <= 0 || K % 64 != 0) { return 0; }
+  return g_deq_once == LTX25_DEQUANT_ONCE_ON || M >= LTX25_DEQUANT_ONCE_AUTO_MIN_M ? 1 : 0;
 }
 
 int ltx25_lora_on_matrix_cores(int M, int K, int N, int rank)

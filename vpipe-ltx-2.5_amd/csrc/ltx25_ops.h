@@ -108,8 +108,8 @@ public:
     return ltx25_lora_on_matrix_cores(M, K, N, rank) != 0;
   }
 
-  // The dequant-once A/B arm (src/ltx25-metal-ops.cc:467-502).
-  void set_dequant_once(bool on) { ltx25_set_dequant_once(on ? 1 : 0); }
+  // The dequant-once arm (src/ltx25-metal-ops.cc:467-502): LTX25_DEQUANT_ONCE_*.
+  void set_dequant_once(int mode) { note(ltx25_set_dequant_once(mode)); }
 
   // src/ltx25-metal-ops.h:151,157.
   void set_i8_gemm(bool on) { ltx25_set_i8_gemm(on ? 1 : 0); }
