@@ -171,7 +171,9 @@ int ltx25_dequant_once_takes(int M, int K, int N);
  * caller scratch and are neither read nor written (either may be NULL).
  * An empty shape (any of M, K, N, rank <= 0) is a no-op, as in the
  * reference. Pointers need only bf16 (2-byte) alignment; 16-byte aligned
- * operands with K % 8 == 0, rank % 8 == 0 and N % 4 == 0 take vector loads.
+ * x, a and y with K % 8 == 0 and N % 8 == 0 take the vector path (when the
+ * rank is not a multiple of 8, b is first copied with its rows zero-padded
+ * to one, into a grow-only scratch).
  * Replaces MetalOps::lora_add (src/ltx25-metal-ops.h:107-133;
  * src/ltx25-metal-ops.cc:989-1004) and its matrix-core pair (:940-987). */
 int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,

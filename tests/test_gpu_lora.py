@@ -37,6 +37,8 @@ SHAPES = [
     ("odd K, odd N (element-wise loads)", 45, 37, 30, 6),
     ("video tokens, rank 64", 1000, 512, 768, 64),
     ("two launches (rank 600)", 70, 256, 192, 600),
+    ("two launches, padded rank (530)", 96, 256, 320, 530),
+    ("N not a multiple of 8 (element-wise y)", 40, 128, 4100, 16),
 ]
 
 

@@ -73,6 +73,8 @@ struct DeviceState {
   size_t i8_bytes = 0;
   void* deq = nullptr;       // dequant-once arm: bf16 [N][K] expansion
   size_t deq_bytes = 0;
+  void* lora_b = nullptr;    // LoRA B padded to a multiple of 8 columns
+  size_t lora_b_bytes = 0;
 };
 
 std::mutex g_mu;
@@ -471,14 +473,33 @@ int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
   DeviceState* ds = nullptr;
   const int rc = current_device(&ds);
   if (rc != LTX25_OK) { return rc; }
-  const bool vec = K % 8 == 0 && rank % 8 == 0 && N % 4 == 0 && aligned16(x) &&
-                   aligned16(a) && aligned16(b) && ((uintptr_t)y & 7u) == 0;
+  // The vector path: 16-byte operand loads and 32-bit buffer offsets. B is
+  // copied with its rank padded to a multiple of 8 when it is not already.
+  const int rank8 = (rank + 7) & ~7;
+  const size_t two_gib = (size_t)1 << 31;
+  const bool vec = K % 8 == 0 && N % 8 == 0 && aligned16(x) && aligned16(a) &&
+                   aligned16(y) && (size_t)M * K * 2 < two_gib &&
+                   (size_t)M * N * 2 < two_gib && (size_t)rank * K * 2 < two_gib &&
+                   (size_t)N * rank8 * 2 < two_gib;
   const uint16_t* pa = (const uint16_t*)a;
   const uint16_t* pb = (const uint16_t*)b;
+  int ldb = rank;
+  if (vec && (rank != rank8 || !aligned16(b))) {
+    {
+      std::lock_guard<std::mutex> lk(g_mu);
+      const int rc2 = grow(&ds->lora_b, &ds->lora_b_bytes, (size_t)N * rank8 * 2);
+      if (rc2 != LTX25_OK) { return rc2; }
+    }
+    const hipError_t e = ltx25::launch_lora_pad(pb, N, rank, rank, (uint16_t*)ds->lora_b, rank8,
+                                                (hipStream_t)stream);
+    if (e != hipSuccess) { return hip_fail(e, "lora pad launch"); }
+    pb = (const uint16_t*)ds->lora_b;
+    ldb = rank8;
+  }
   for (int c = 0; c < rank; c += ltx25::kLoraMaxRank) {
     const int rp = rank - c < ltx25::kLoraMaxRank ? rank - c : ltx25::kLoraMaxRank;
     const hipError_t e = ltx25::launch_lora((const uint16_t*)x, pa + (size_t)c * K, pb + c,
-                                            (uint16_t*)y, M, K, N, rp, rank, vec,
+                                            (uint16_t*)y, M, K, N, rp, ldb, vec,
                                             ds->cu_count, (hipStream_t)stream);
     if (e != hipSuccess) { return hip_fail(e, "lora launch"); }
   }

@@ -110,13 +110,19 @@ hipError_t launch_skinny(const GemmDesc& d, const SkinnyPlan& plan, float* parti
 // The low-rank adapter delta y += (x . A^T) . B^T (lora.hip). One launch
 // covers at most kLoraMaxRank adapter columns: `a` points at the pass's
 // first row of A [rank][K], `b` at its first column of B [N][ldb]. `vec`
-// selects 16-byte operand loads (K % 8 == 0, ldb % 8 == 0, N % 4 == 0 and
-// aligned pointers).
+// selects 16-byte operand loads (K % 8 == 0, ldb % 8 == 0, N % 8 == 0,
+// aligned pointers, every operand under 2 GiB, and B's columns zero from
+// `rank` up to the next multiple of 8).
 constexpr int kLoraMaxRank = 512;
-int lora_splits(int M, int N, int cu_count);
+int lora_splits(int M, int N, int rank, int cu_count);
 hipError_t launch_lora(const uint16_t* x, const uint16_t* a, const uint16_t* b,
                        uint16_t* y, int M, int K, int N, int rank, int ldb,
                        bool vec, int cu_count, hipStream_t stream);
+// B [rows][cols] (row stride ld_src) -> [rows][ld_dst] with zero columns past
+// `cols`: the vector path's copy of an adapter whose rank is not a multiple
+// of 8.
+hipError_t launch_lora_pad(const uint16_t* src, int rows, int cols, int ld_src, uint16_t* dst,
+                           int ld_dst, hipStream_t stream);
 
 hipError_t launch_bias_add(uint16_t* y, const void* bias, int bias_type,
                            int M, int N, hipStream_t stream);

@@ -33,6 +33,7 @@ namespace {
 constexpr int kLoraRows = 32;
 constexpr int kLoraWaves = 4;
 constexpr int kLoraThreads = kLoraWaves * 64;
+constexpr int kYsRow = 128 + 8;   // bf16 per row of a y staging tile (16 B pad)
 
 struct LoraParams {
   const uint16_t* x;
@@ -45,26 +46,45 @@ struct LoraParams {
   int n_split;  // columns of y per workgroup along grid.y, multiple of 32
 };
 
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// Raw buffer resource over `bytes` bytes: a load at an offset past the end
+// returns zeros and a store there is dropped, so out-of-range lanes need no
+// branch (a branch around a load makes the compiler wait for every
+// outstanding load where the paths join, which would drain the pipelines
+// below). Offsets are 32-bit: the host takes this path only for operands
+// under 2 GiB.
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, size_t bytes)
+{
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
+                                           (int)(uint32_t)bytes, 0x00020000);
+}
+
 // Eight bf16 of row `row`, columns k..k+7, of a row-major matrix with
-// `rows` x `cols` valid elements and row stride `ld`; zero outside. VEC
-// requires cols % 8 == 0 and 16-byte aligned rows, so a chunk is either
-// wholly inside or wholly outside.
-template <bool VEC>
-__device__ __forceinline__ bf16x8 frag8(const uint16_t* p, int row, int rows,
-                                        int k, int cols, long ld)
+// `rows` x `cols` valid elements and row stride `ld`; zero outside.
+// Vector form: cols % 8 == 0 and 16-byte aligned rows, so a chunk is
+// wholly inside or wholly outside; one 16-byte buffer load.
+__device__ __forceinline__ bf16x8 frag8v(__amdgpu_buffer_rsrc_t r, int row, int rows, int k,
+                                         int cols, int ld)
+{
+  const uint32_t off = (row < rows && k < cols) ? (uint32_t)(row * ld + k) * 2u : kOob;
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+// Element-wise form for any shape and 2-byte alignment.
+__device__ __forceinline__ bf16x8 frag8s(const uint16_t* p, int row, int rows, int k, int cols,
+                                         long ld)
 {
   i32x4 v = {0, 0, 0, 0};
-  if constexpr (VEC) {
-    if (row < rows && k < cols) { v = *(const i32x4*)(p + (size_t)row * ld + k); }
-  } else {
-    if (row < rows) {
-      const uint16_t* q = p + (size_t)row * ld;
+  if (row < rows) {
+    const uint16_t* q = p + (size_t)row * ld;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = (k + 2 * i < cols) ? q[k + 2 * i] : 0u;
-        const uint32_t hi = (k + 2 * i + 1 < cols) ? q[k + 2 * i + 1] : 0u;
-        v[i] = (int)(lo | (hi << 16));
-      }
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = (k + 2 * i < cols) ? q[k + 2 * i] : 0u;
+      const uint32_t hi = (k + 2 * i + 1 < cols) ? q[k + 2 * i + 1] : 0u;
+      v[i] = (int)(lo | (hi << 16));
     }
   }
   return __builtin_bit_cast(bf16x8, v);
@@ -77,75 +97,117 @@ __global__ __launch_bounds__(kLoraThreads) void lora_kernel(LoraParams p)
   constexpr int RP = 32 * RB;        // rank padded to the MFMA block
   constexpr int RS = RP + 8;         // bf16 per LDS row of r (16-byte pad)
   constexpr int FS = RP + 4;         // f32 per LDS row of the partials
-  __shared__ __attribute__((aligned(16))) float red[kLoraRows * FS];
+  __shared__ __attribute__((aligned(16))) float red[RB >= 4 ? 4 : kLoraRows * FS];
   __shared__ __attribute__((aligned(16))) uint16_t rl[kLoraRows * RS];
+  // per-wave y staging tiles of the vector path (unused by the other)
+  __shared__ __attribute__((aligned(16))) uint16_t ystage[VEC ? kLoraWaves * kLoraRows * kYsRow : 8];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int l32 = lane & 31;
   const int hi = lane >> 5;
   const int m0 = blockIdx.x * kLoraRows;
+  const auto rx = rsrc(p.x, (size_t)p.M * p.K * 2);
+  const auto ra = rsrc(p.a, (size_t)p.rank * p.K * 2);
+  const auto rbm = rsrc(p.b, ((size_t)(p.N - 1) * p.ldb + ((p.rank + 7) & ~7)) * 2);
+  const auto ry = rsrc(p.y, (size_t)p.M * p.N * 2);
+  auto xfrag = [&](int k) {
+    if constexpr (VEC) { return frag8v(rx, m0 + l32, p.M, k, p.K, p.K); }
+    else { return frag8s(p.x, m0 + l32, p.M, k, p.K, p.K); }
+  };
+  auto afrag = [&](int rb, int k) {
+    if constexpr (VEC) { return frag8v(ra, rb * 32 + l32, p.rank, k, p.K, p.K); }
+    else { return frag8s(p.a, rb * 32 + l32, p.rank, k, p.K, p.K); }
+  };
 
-  // ---- phase 1: r^T[i][m] = sum_k A[i][k] x[m][k], K split over waves ----
-  f32x16 acc[RB];
+  // ---- phase 1: r^T[i][m] = sum_k A[i][k] x[m][k] ---------------------------
+  // Narrow adapters (RB < 4) split K over the four waves and add the
+  // partials through LDS in wave order; wide ones split the rank blocks
+  // (RB / 4 per wave, each over all of K), so every wave owns its columns of
+  // r and no reduction is needed. Either way the K steps of 16 run through
+  // a ring of D1 register slots: slot d holds one step's fragments and is
+  // refilled with the step D1 ahead as soon as its MFMAs have been issued.
+  // A step past the end loads zeros (k = K is outside every row).
+  constexpr bool kRankSplit = RB >= 4;
+  constexpr int RBW = kRankSplit ? RB / kLoraWaves : RB;   // rank blocks per wave
+  constexpr int D1 = kRankSplit ? 4 : 8 / RB;
+  const int rb0 = kRankSplit ? wave * RBW : 0;
+  f32x16 acc[RBW];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
+  for (int rb = 0; rb < RBW; ++rb) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) { acc[rb][r] = 0.0f; }
   }
-  // K steps of 16, dealt round-robin to the waves; U steps' fragments are
-  // loaded before their MFMAs so several loads are in flight per wave.
-  // A step past the end loads zeros (k = K is outside every row).
-  constexpr int U = RB <= 2 ? 4 : (RB <= 4 ? 2 : 1);
   const int steps = (p.K + 15) / 16;
-  const int nloc = (steps - wave + kLoraWaves - 1) / kLoraWaves;
-  for (int j = 0; j < nloc; j += U) {
-    bf16x8 xf[U];
-    bf16x8 af[U][RB];
+  const int nloc = kRankSplit ? steps : (steps - wave + kLoraWaves - 1) / kLoraWaves;
+  auto kstep = [&](int j) {
+    if (j >= nloc) { return p.K; }
+    return (kRankSplit ? j : wave + j * kLoraWaves) * 16 + hi * 8;
+  };
+  bf16x8 xf[D1];
+  bf16x8 af[D1][RBW];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = j + u < nloc ? (wave + (j + u) * kLoraWaves) * 16 + hi * 8 : p.K;
-      xf[u] = frag8<VEC>(p.x, m0 + l32, p.M, k, p.K, p.K);
+  for (int d = 0; d < D1; ++d) {
+    const int k = kstep(d);
+    xf[d] = xfrag(k);
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        af[u][rb] = frag8<VEC>(p.a, rb * 32 + l32, p.rank, k, p.K, p.K);
-      }
-    }
+    for (int rb = 0; rb < RBW; ++rb) { af[d][rb] = afrag(rb0 + rb, k); }
+  }
+  for (int j0 = 0; j0 < nloc; j0 += D1) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int d = 0; d < D1; ++d) {
+      if (j0 + d >= nloc) { break; }
+      const int kn = kstep(j0 + d + D1);
+      const bf16x8 xc = xf[d];
+      xf[d] = xfrag(kn);
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[u][rb], xf[u], acc[rb], 0, 0, 0);
+      for (int rb = 0; rb < RBW; ++rb) {
+        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[d][rb], xc, acc[rb], 0, 0, 0);
+        af[d][rb] = afrag(rb0 + rb, kn);
       }
     }
   }
 
   // Lane l, register r of block rb holds r^T[i][m] with m = l & 31 and
-  // i = 32 rb + 8 (r / 4) + 4 (l / 32) + r % 4. Waves add in order 0..3;
-  // the last rounds to bf16 into rl[m][i].
-  for (int w = 0; w < kLoraWaves; ++w) {
-    if (wave == w) {
+  // i = 32 rb + 8 (r / 4) + 4 (l / 32) + r % 4; r lands in rl[m][i] as bf16.
+  auto put_r = [&](int rb, int g, f32x4 v) {
+    uint2 o;
+    o.x = pack_bf16x2(v[0], v[1]);
+    o.y = pack_bf16x2(v[2], v[3]);
+    *(uint2*)(rl + l32 * RS + rb * 32 + g * 8 + hi * 4) = o;
+  };
+  if constexpr (kRankSplit) {
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
+    for (int rb = 0; rb < RBW; ++rb) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int i = rb * 32 + g * 8 + hi * 4;
-          float* dst = red + l32 * FS + i;
-          f32x4 v = {acc[rb][4 * g], acc[rb][4 * g + 1], acc[rb][4 * g + 2],
-                     acc[rb][4 * g + 3]};
-          if (w > 0) { v += *(const f32x4*)dst; }
-          if (w < kLoraWaves - 1) {
-            *(f32x4*)dst = v;
-          } else {
-            uint2 o;
-            o.x = pack_bf16x2(v[0], v[1]);
-            o.y = pack_bf16x2(v[2], v[3]);
-            *(uint2*)(rl + l32 * RS + i) = o;
-          }
-        }
+      for (int g = 0; g < 4; ++g) {
+        put_r(rb0 + rb, g, f32x4{acc[rb][4 * g], acc[rb][4 * g + 1], acc[rb][4 * g + 2],
+                                 acc[rb][4 * g + 3]});
       }
     }
     __syncthreads();
+  } else {
+    // waves add in order 0..3 through LDS; the last rounds to bf16
+    for (int w = 0; w < kLoraWaves; ++w) {
+      if (wave == w) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float* dst = red + l32 * FS + rb * 32 + g * 8 + hi * 4;
+            f32x4 v = {acc[rb][4 * g], acc[rb][4 * g + 1], acc[rb][4 * g + 2],
+                       acc[rb][4 * g + 3]};
+            if (w > 0) { v += *(const f32x4*)dst; }
+            if (w < kLoraWaves - 1) {
+              *(f32x4*)dst = v;
+            } else {
+              put_r(rb, g, v);
+            }
+          }
+        }
+      }
+      __syncthreads();
+    }
   }
 
   // ---- phase 2: y^T[n][m] = y^T[n][m] + sum_j B[n][j] r[m][j] -----------
@@ -154,44 +216,121 @@ __global__ __launch_bounds__(kLoraThreads) void lora_kernel(LoraParams p)
   const bool row_ok = row < p.M;
   const int n_lo = blockIdx.y * p.n_split;
   const int n_hi = min(p.N, n_lo + p.n_split);
-  for (int nb = n_lo + wave * 32; nb < n_hi; nb += kLoraWaves * 32) {
-    f32x16 c;
-    uint16_t* yrow = p.y + (size_t)row * p.N;
+  uint16_t* yrow = p.y + (size_t)row * p.N;
+  if constexpr (VEC) {
+    // Super blocks of 128 columns (four 32-column MFMA blocks), dealt
+    // round-robin to the waves. A super block's y tile (32 rows x 256 B)
+    // moves between HBM and a per-wave LDS tile as whole row segments (16
+    // lanes per row, 16 B each) and between LDS and the accumulators in the
+    // MFMA layout. Its HBM loads are issued kDy super blocks ahead. B's
+    // fragments rotate per 32-column block: slot s is refilled with the
+    // next block's rank step s as soon as its MFMA has been issued.
+    constexpr int KS = 2 * RB;                      // 16-deep rank steps
+    constexpr int kSb = 4;                          // MFMA blocks per super block
+    constexpr int kSbStride = kLoraWaves * kSb * 32;
+    constexpr int kDy = 2;
+    // B's rows are zero-padded to a multiple of 8 (the host pads a copy when
+    // the adapter's rank is not), so an 8-column chunk below rank8 is whole.
+    const int rank8 = (p.rank + 7) & ~7;
+    uint16_t* ys = ystage + wave * (kLoraRows * kYsRow);
+    const int lr = lane >> 4;         // row within a group of 4 (HBM side)
+    const int lc = (lane & 15) * 8;   // column of this lane's 16 B (HBM side)
+    auto yoff16 = [&](int sb, int i) {
+      const int r = m0 + 4 * i + lr;
+      const int n = sb + lc;
+      return (r < p.M && n < n_hi) ? (uint32_t)(r * p.N + n) * 2u : kOob;
+    };
+    // B fragments in NB banks: block cb of a super block uses bank cb % NB,
+    // and a bank's slot s is refilled with the block NB ahead.
+    constexpr int NB = RB <= 2 ? 4 : (RB <= 8 ? 2 : 1);
+    i32x4 yv[kDy][8];
+    bf16x8 bf[NB][KS];
+    const int sb0 = n_lo + wave * kSb * 32;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int n = nb + g * 8 + hi * 4;
-      if constexpr (VEC) {
-        uint2 v = {0u, 0u};
-        if (row_ok && n < n_hi) { v = *(const uint2*)(yrow + n); }
-        c[4 * g + 0] = __uint_as_float(v.x << 16);
-        c[4 * g + 1] = __uint_as_float(v.x & 0xffff0000u);
-        c[4 * g + 2] = __uint_as_float(v.y << 16);
-        c[4 * g + 3] = __uint_as_float(v.y & 0xffff0000u);
-      } else {
+    for (int d = 0; d < kDy; ++d) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        yv[d][i] = __builtin_amdgcn_raw_buffer_load_b128(ry, (int)yoff16(sb0 + d * kSbStride, i),
+                                                         0, 0);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        bf[b][s] = frag8v(rbm, sb0 + b * 32 + l32, n_hi, s * 16 + hi * 8, rank8, p.ldb);
+      }
+    }
+    for (int base = sb0; base < n_hi; base += kDy * kSbStride) {
+#pragma unroll
+      for (int d = 0; d < kDy; ++d) {
+        const int sb = base + d * kSbStride;
+        if (sb >= n_hi) { break; }
+        // HBM rows -> LDS tile, then this slot's next loads
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          *(i32x4*)(ys + (4 * i + lr) * kYsRow + lc) = yv[d][i];
+          yv[d][i] = __builtin_amdgcn_raw_buffer_load_b128(
+              ry, (int)yoff16(sb + kDy * kSbStride, i), 0, 0);
+        }
+#pragma unroll
+        for (int cb = 0; cb < kSb; ++cb) {
+          const int nxt = cb + NB < kSb ? sb + (cb + NB) * 32 : sb + kSbStride + (cb + NB - kSb) * 32;
+          uint16_t* yt = ys + l32 * kYsRow + cb * 32 + hi * 4;
+          f32x16 c;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const u32x2 v = *(const u32x2*)(yt + g * 8);
+            c[4 * g + 0] = __uint_as_float(v.x << 16);
+            c[4 * g + 1] = __uint_as_float(v.x & 0xffff0000u);
+            c[4 * g + 2] = __uint_as_float(v.y << 16);
+            c[4 * g + 3] = __uint_as_float(v.y & 0xffff0000u);
+          }
+#pragma unroll
+          for (int s = 0; s < KS; ++s) {
+            if (s < ksteps) {
+              const bf16x8 rfr = *(const bf16x8*)(rl + l32 * RS + s * 16 + hi * 8);
+              c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[cb % NB][s], rfr, c, 0, 0, 0);
+            }
+            bf[cb % NB][s] = frag8v(rbm, nxt + l32, n_hi, s * 16 + hi * 8, rank8, p.ldb);
+          }
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            u32x2 o;
+            o.x = pack_bf16x2(c[4 * g + 0], c[4 * g + 1]);
+            o.y = pack_bf16x2(c[4 * g + 2], c[4 * g + 3]);
+            *(u32x2*)(yt + g * 8) = o;
+          }
+        }
+        // LDS tile -> HBM rows
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const i32x4 o = *(const i32x4*)(ys + (4 * i + lr) * kYsRow + lc);
+          __builtin_amdgcn_raw_buffer_store_b128(o, ry, (int)yoff16(sb, i), 0, 0);
+        }
+      }
+    }
+  } else {
+    for (int nb = n_lo + wave * 32; nb < n_hi; nb += kLoraWaves * 32) {
+      f32x16 c;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = nb + g * 8 + hi * 4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           c[4 * g + e] = (row_ok && n + e < n_hi) ? bf16_to_f32(yrow[n + e]) : 0.0f;
         }
       }
-    }
-    for (int s = 0; s < ksteps; ++s) {
-      const int k = s * 16 + hi * 8;
-      const bf16x8 bfr = frag8<VEC>(p.b, nb + l32, n_hi, k, p.rank, p.ldb);
-      const bf16x8 rfr = *(const bf16x8*)(rl + l32 * RS + k);
-      c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr, rfr, c, 0, 0, 0);
-    }
-    if (row_ok) {
+      for (int s = 0; s < ksteps; ++s) {
+        const int k = s * 16 + hi * 8;
+        const bf16x8 bfr = frag8s(p.b, nb + l32, n_hi, k, p.rank, p.ldb);
+        const bf16x8 rfr = *(const bf16x8*)(rl + l32 * RS + k);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr, rfr, c, 0, 0, 0);
+      }
+      if (row_ok) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = nb + g * 8 + hi * 4;
-        if constexpr (VEC) {
-          if (n < n_hi) {
-            uint2 o;
-            o.x = pack_bf16x2(c[4 * g + 0], c[4 * g + 1]);
-            o.y = pack_bf16x2(c[4 * g + 2], c[4 * g + 3]);
-            *(uint2*)(yrow + n) = o;
-          }
-        } else {
+        for (int g = 0; g < 4; ++g) {
+          const int n = nb + g * 8 + hi * 4;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             if (n + e < n_hi) { yrow[n + e] = f32_to_bf16(c[4 * g + e]); }
@@ -213,18 +352,42 @@ hipError_t launch_rb(const LoraParams& p, bool vec, dim3 grid, hipStream_t strea
   return hipGetLastError();
 }
 
+// dst[r][c] = c < cols ? src[r][c] : 0 for c < ld_dst: B with its rank
+// padded to a multiple of 8 columns, so the vector path can load it.
+__global__ void lora_pad_kernel(const uint16_t* __restrict__ src, int rows, int cols,
+                                int ld_src, uint16_t* __restrict__ dst, int ld_dst)
+{
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)rows * ld_dst) { return; }
+  const int r = (int)(i / ld_dst);
+  const int c = (int)(i % ld_dst);
+  dst[i] = c < cols ? src[(size_t)r * ld_src + c] : (uint16_t)0;
+}
+
 }  // namespace
 
-// Column split along grid.y: enough workgroups to cover the CUs when the
-// token count is small, but never fewer than 1024 columns per workgroup,
-// because every split recomputes phase 1 for its row block.
-int lora_splits(int M, int N, int cu_count)
+hipError_t launch_lora_pad(const uint16_t* src, int rows, int cols, int ld_src, uint16_t* dst,
+                           int ld_dst, hipStream_t stream)
+{
+  const size_t n = (size_t)rows * ld_dst;
+  if (n == 0) { return hipSuccess; }
+  lora_pad_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(src, rows, cols, ld_src, dst,
+                                                                     ld_dst);
+  return hipGetLastError();
+}
+
+// Column split along grid.y. Every split recomputes phase 1 for its row
+// block (x and all of A again), so a wide adapter gets just enough
+// workgroups to cover the CUs once; a narrow one, whose phase 2 is bound by
+// y traffic and wants waves in flight, gets two per CU. Never fewer than
+// 1024 columns per workgroup.
+int lora_splits(int M, int N, int rank, int cu_count)
 {
   const int mtiles = (M + kLoraRows - 1) / kLoraRows;
-  if (mtiles >= cu_count) { return 1; }
-  const int want = (cu_count + mtiles - 1) / mtiles;
+  const int per_cu = rank > 128 ? 1 : 2;
+  const int want = per_cu * cu_count / mtiles;
   const int cap = (N + 1023) / 1024;
-  return want < cap ? want : cap;
+  return want < 1 ? 1 : (want < cap ? want : cap);
 }
 
 hipError_t launch_lora(const uint16_t* x, const uint16_t* a, const uint16_t* b,
@@ -232,9 +395,11 @@ hipError_t launch_lora(const uint16_t* x, const uint16_t* a, const uint16_t* b,
                        bool vec, int cu_count, hipStream_t stream)
 {
   if (rank <= 0 || rank > kLoraMaxRank) { return hipErrorInvalidValue; }
-  const int splits = lora_splits(M, N, cu_count);
+  const int splits = lora_splits(M, N, rank, cu_count);
   int n_split = (N + splits - 1) / splits;
-  n_split = (n_split + 31) / 32 * 32;
+  // whole super-block strides (4 waves x 128 columns) where N allows
+  const int quantum = N >= 512 ? 512 : 32;
+  n_split = (n_split + quantum - 1) / quantum * quantum;
   const int gy = (N + n_split - 1) / n_split;
   LoraParams p{x, a, b, y, M, K, N, rank, ldb, n_split};
   const dim3 grid((unsigned)((M + kLoraRows - 1) / kLoraRows), (unsigned)gy);
