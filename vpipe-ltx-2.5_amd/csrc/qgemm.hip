@@ -323,7 +323,7 @@ qgemm_kernel(KParams p)
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr[buf][i], bfr[buf][j],
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[buf][j], afr[buf][i],
                                                            acc[i][j], 0, 0, 0);
       }
     }
@@ -400,28 +400,97 @@ qgemm_kernel(KParams p)
     step(s, std::false_type{}, std::false_type{});
   }
 
-  // Accumulator layout of the 32x32 f32 MFMA result: lane l, register r
-  // holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int n = n0 + wn * WTN + j * 32 + (lane & 31);
-    float bv = 0.0f;
-    if (!SPLIT && n < p.N) { bv = load_bias(p.bias, p.bias_type, n); }
+  // Accumulator layout. The MFMAs take the weight fragment as their first
+  // operand, so block (i, j) holds the transposed 32x32 product: lane l,
+  // register r is row m = 32 i + l % 32 of the wave's sub-tile and column
+  // n = 32 j + 8 (r / 4) + 4 (l / 32) + r % 4 -- registers 4g..4g+3 are four
+  // consecutive columns of one row.
+  const int lrow = lane & 31;
+  const int lcol = (lane >> 5) * 4;
+  if constexpr (SPLIT) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const int mb = m0 + wm * WTM + i * 32 + (lane >> 5) * 4;
+      const int m = m0 + wm * WTM + i * 32 + lrow;
+      if (m >= p.M) { continue; }
+      float* prow = p.partial + ((size_t)split * p.M + m) * p.N;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = mb + (r >> 2) * 8 + (r & 3);
-        if (m < p.M && n < p.N) {
-          float v = acc[i][j][r];
-          if constexpr (SPLIT) {
-            p.partial[((size_t)split * p.M + m) * p.N + n] = v;
+      for (int j = 0; j < FN; ++j) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + wn * WTN + j * 32 + g * 8 + lcol;
+          const f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                           acc[i][j][4 * g + 3]};
+          if ((p.N & 3) == 0 && n + 3 < p.N) {
+            *(f32x4*)(prow + n) = v;
           } else {
-            v += bv;
-            if (p.epilogue == kEpiGelu) { v = gelu_tanh(v); }
-            p.y[(size_t)m * p.N + n] = f32_to_bf16(v);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              if (n + t < p.N) { prow[n + t] = v[t]; }
+            }
           }
+        }
+      }
+    }
+  } else {
+    // Bias and epilogue in f32, one rounding to bf16 into an LDS copy of
+    // the tile (rows [0, BM/2) in the X stages, the rest in the weight
+    // stages), then the tile leaves as 16-byte row segments.
+    constexpr int EP = BN + 8;   // bf16 per staged row (16-byte pad)
+    static_assert((BM / 2) * EP <= 2 * BM * kLdsRow && (BM / 2) * EP <= 2 * BN * kLdsRow,
+                  "the staged output tile must fit the operand stages");
+    uint16_t* const stage_lo = &lds_a[0][0];
+    uint16_t* const stage_hi = &lds_b[0][0];
+    __syncthreads();   // every wave is done reading the operand tiles
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      float bv[4][4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int n = n0 + wn * WTN + j * 32 + g * 8 + lcol + t;
+          bv[g][t] = n < p.N ? load_bias(p.bias, p.bias_type, n) : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * WTM + i * 32 + lrow;
+        uint16_t* srow = r < BM / 2 ? stage_lo + r * EP : stage_hi + (r - BM / 2) * EP;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float v[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            v[t] = acc[i][j][4 * g + t] + bv[g][t];
+            if (p.epilogue == kEpiGelu) { v[t] = gelu_tanh(v[t]); }
+          }
+          *(uint2*)(srow + wn * WTN + j * 32 + g * 8 + lcol) =
+              make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        }
+      }
+    }
+    __syncthreads();
+    constexpr int CPR = BN / 8;   // 16-byte chunks per row
+    const bool vec_rows = (p.N & 7) == 0;
+#pragma unroll 4
+    for (int q = tid; q < BM * CPR; q += NT) {
+      const int r = q / CPR;
+      const int c = (q % CPR) * 8;
+      const int m = m0 + r;
+      const int n = n0 + c;
+      if (m >= p.M || n >= p.N) { continue; }
+      const uint16_t* srow = r < BM / 2 ? stage_lo + r * EP : stage_hi + (r - BM / 2) * EP;
+      const uint4 v = *(const uint4*)(srow + c);
+      uint16_t* dst = p.y + (size_t)m * p.N + n;
+      if (vec_rows && n + 8 <= p.N) {
+        *(uint4*)dst = v;
+      } else {
+        const uint16_t e[8] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y,
+                               (uint16_t)(v.y >> 16), (uint16_t)v.z, (uint16_t)(v.z >> 16),
+                               (uint16_t)v.w, (uint16_t)(v.w >> 16)};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          if (n + t < p.N) { dst[t] = e[t]; }
         }
       }
     }
