@@ -62,35 +62,6 @@ struct KParams {
   int tiles_m, tiles_n;
 };
 
-// Workgroup id -> (tile_m, tile_n). Consecutive workgroup ids are dealt
-// round-robin to the 8 XCDs, so the id is first remapped so that each XCD
-// receives a contiguous range of tiles, then the range is walked in groups
-// of 8 M-tiles: the workgroups an XCD runs at once share X and W tiles in
-// that XCD's L2.
-__device__ __forceinline__ void map_tile(int bid, int tiles_m, int tiles_n,
-                                         int& tm, int& tn)
-{
-  const int total = tiles_m * tiles_n;
-  const int total8 = total & ~7;
-  int pid = bid;
-  if (bid < total8) { pid = (bid & 7) * (total8 >> 3) + (bid >> 3); }
-  constexpr int kGroupM = 8;
-  const int per_group = kGroupM * tiles_n;
-  const int gid = pid / per_group;
-  const int first_m = gid * kGroupM;
-  const int gsz = min(tiles_m - first_m, kGroupM);
-  const int r = pid - gid * per_group;
-  tm = first_m + r % gsz;
-  tn = r / gsz;
-}
-
-__device__ __forceinline__ float load_bias(const void* bias, int type, int n)
-{
-  if (type == kBiasBf16) { return bf16_to_f32(((const uint16_t*)bias)[n]); }
-  if (type == kBiasF32) { return ((const float*)bias)[n]; }
-  return 0.0f;
-}
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p,
                                                            size_t bytes)
 {
