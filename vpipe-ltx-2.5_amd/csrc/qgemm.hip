@@ -40,13 +40,20 @@ namespace {
 // Wave grid of the 256 x 256 tile.
 constexpr int kTallWM = 2;
 constexpr int kTallWN = 4;
-constexpr int kBK = 64;             // K per main-loop step
+constexpr int kBK = 64;             // K per main-loop step (bf16 activations)
+// BITS value of the int8 x int8 -> int32 GEMM (the int8 tier): both
+// operands are int8 rows, 128 of K per step in the same 128-byte LDS rows.
+constexpr int kI8Ops = 1;
 constexpr int kLdsRow = kBK + 8;    // bf16 per LDS row: 144 B pitch keeps
                                     // the 16 B fragment reads conflict-free
 
 struct KParams {
   const uint16_t* x;
-  const uint8_t* wq;       // codes as bytes (bits 8 or 4)
+  const int8_t* xq;        // int8 activations (kI8Ops)
+  const float* sx;         // per-row activation scales (kI8Ops)
+  const float* sw;         // per-column weight scales (kI8Ops)
+  int32_t* acc_out;        // optional raw int32 accumulators (kI8Ops)
+  const uint8_t* wq;       // codes as bytes (bits 8 or 4), or int8 weights
   const uint16_t* wd;      // dense bf16 weight (bits 16)
   const uint16_t* scales;
   const uint16_t* qbias;
@@ -128,11 +135,14 @@ qgemm_kernel(KParams p)
   constexpr int FN = WTN / 32;
   constexpr int A_LD = BM * 8 / NT;                  // 16 B chunks / thread
   constexpr int A_RSTEP = NT / 8;
-  constexpr int B_CPR = BITS == 16 ? 8 : kBK * BITS / 8 / 16;  // chunks/row
+  constexpr bool I8 = BITS == kI8Ops;
+  constexpr bool QUANT = BITS == 8 || BITS == 4;     // group-affine codes
+  constexpr int SK = I8 ? 2 * kBK : kBK;             // K elements per step
+  constexpr int XB = I8 ? 1 : 2;                     // bytes per activation
+  constexpr int B_CPR = QUANT ? kBK * BITS / 8 / 16 : 8;  // chunks/row
   constexpr int B_LD = BN * B_CPR / NT;
   constexpr int B_RSTEP = NT / B_CPR;
-  constexpr int CPC = BITS == 16 ? 8 : 128 / BITS;   // codes per chunk
-  constexpr bool QUANT = BITS != 16;
+  constexpr int CPC = QUANT ? 128 / BITS : 8;        // codes per chunk (16 B in LDS units)
   static_assert(A_LD >= 1 && B_LD >= 1, "tile too small for the thread count");
 
   __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * kLdsRow];
@@ -151,7 +161,7 @@ qgemm_kernel(KParams p)
   const int split = SPLIT ? (int)blockIdx.y : 0;
   const int kbeg = split * p.k_chunk;
   const int kend = min(p.K, kbeg + p.k_chunk);
-  const int nsteps = kend > kbeg ? (kend - kbeg) / kBK : 0;
+  const int nsteps = kend > kbeg ? (kend - kbeg) / SK : 0;
 
   const int a_c = tid & 7;
   const int a_r = tid >> 3;
@@ -160,10 +170,11 @@ qgemm_kernel(KParams p)
 
   // Buffer resources and per-thread byte offsets, fixed for the whole loop;
   // each step adds a uniform K offset (an SGPR).
-  const size_t wrow_bytes = (size_t)p.K * (QUANT ? BITS : 16) / 8;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, (size_t)p.M * p.K * 2);
+  const size_t wrow_bytes = (size_t)p.K * (QUANT ? BITS : (I8 ? 8 : 16)) / 8;
+  const __amdgpu_buffer_rsrc_t xr =
+      make_rsrc(I8 ? (const void*)p.xq : (const void*)p.x, (size_t)p.M * p.K * XB);
   const __amdgpu_buffer_rsrc_t wr =
-      make_rsrc(QUANT ? (const void*)p.wq : (const void*)p.wd, (size_t)p.N * wrow_bytes);
+      make_rsrc(QUANT || I8 ? (const void*)p.wq : (const void*)p.wd, (size_t)p.N * wrow_bytes);
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(p.scales, (size_t)p.N * p.gcols * 2);
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(p.qbias, (size_t)p.N * p.gcols * 2);
   uint32_t a_off[A_LD];
@@ -171,7 +182,7 @@ qgemm_kernel(KParams p)
   uint32_t s_off[B_LD];
 #pragma unroll
   for (int i = 0; i < A_LD; ++i) {
-    a_off[i] = (uint32_t)(((size_t)(m0 + a_r + A_RSTEP * i) * p.K + a_c * 8) * 2);
+    a_off[i] = (uint32_t)((size_t)(m0 + a_r + A_RSTEP * i) * p.K * XB + a_c * 16);
   }
 #pragma unroll
   for (int i = 0; i < B_LD; ++i) {
@@ -187,12 +198,12 @@ qgemm_kernel(KParams p)
 
   auto load_a = [&](int k) {
 #pragma unroll
-    for (int i = 0; i < A_LD; ++i) { areg[i] = buf_load16(xr, a_off[i], (uint32_t)k * 2); }
+    for (int i = 0; i < A_LD; ++i) { areg[i] = buf_load16(xr, a_off[i], (uint32_t)k * XB); }
   };
   auto load_b = [&](int k) {
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
-      breg[i] = buf_load16(wr, b_off[i], (uint32_t)k * (QUANT ? BITS : 16) / 8);
+      breg[i] = buf_load16(wr, b_off[i], (uint32_t)k * (QUANT ? BITS : (I8 ? 8 : 16)) / 8);
       if constexpr (QUANT) {
         const uint32_t so = (uint32_t)(k >> p.gshift) * 2;
         sraw[i] = buf_load2(sr, s_off[i], so);
@@ -262,13 +273,14 @@ qgemm_kernel(KParams p)
 
   auto store_b = [&](int st) { store_b_rows(st, 0, B_LD); };
 
-  f32x16 acc[FM][FN];
+  using AccT = std::conditional_t<I8, i32x16, f32x16>;
+  AccT acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) { acc[i][j][r] = 0.0f; }
+      for (int r = 0; r < 16; ++r) { acc[i][j][r] = 0; }
     }
   }
 
@@ -294,8 +306,15 @@ qgemm_kernel(KParams p)
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[buf][j], afr[buf][i],
-                                                           acc[i][j], 0, 0, 0);
+        if constexpr (I8) {
+          // 32 int8 of K per lane pair: the same 16 bytes a bf16 fragment holds
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+              __builtin_bit_cast(i32x4, bfr[buf][j]), __builtin_bit_cast(i32x4, afr[buf][i]),
+              acc[i][j], 0, 0, 0);
+        } else {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[buf][j], afr[buf][i],
+                                                             acc[i][j], 0, 0, 0);
+        }
       }
     }
   };
@@ -335,14 +354,14 @@ qgemm_kernel(KParams p)
     read_frags(st, 2, 0);
     mfma_all(1);
     if constexpr (kStore) { store_b_rows(nst, 0, kB1); }
-    if constexpr (kLoad) { load_a(kbeg + (s + 2) * kBK); }
+    if constexpr (kLoad) { load_a(kbeg + (s + 2) * SK); }
     interleave<kMf, kRd, kStore ? kB1 * kWrChunk : 0, kStore ? kB1 * kValuChunk : 0,
                kLoad ? A_LD : 0>();
     __builtin_amdgcn_sched_barrier(0);
     read_frags(st, 3, 1);
     mfma_all(0);
     if constexpr (kStore) { store_b_rows(nst, kB1, B_LD); }
-    if constexpr (kLoad) { load_b(kbeg + (s + 2) * kBK); }
+    if constexpr (kLoad) { load_b(kbeg + (s + 2) * SK); }
     interleave<kMf, kRd, kStore ? (B_LD - kB1) * kWrChunk : 0,
                kStore ? (B_LD - kB1) * kValuChunk : 0, kLoad ? kGlB : 0>();
     __builtin_amdgcn_sched_barrier(0);
@@ -359,7 +378,7 @@ qgemm_kernel(KParams p)
     load_regs(kbeg);
     store_a(0);
     store_b(0);
-    if (nsteps > 1) { load_regs(kbeg + kBK); }
+    if (nsteps > 1) { load_regs(kbeg + SK); }
     __syncthreads();
     read_frags(0, 0, 0);
     int s = 0;
@@ -415,25 +434,48 @@ qgemm_kernel(KParams p)
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       float bv[4][4];
+      float swv[4][4];   // int8 GEMM: per-column weight scales
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int n = n0 + wn * WTN + j * 32 + g * 8 + lcol + t;
           bv[g][t] = n < p.N ? load_bias(p.bias, p.bias_type, n) : 0.0f;
+          swv[g][t] = I8 && n < p.N ? p.sw[n] : 0.0f;
         }
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int r = wm * WTM + i * 32 + lrow;
         uint16_t* srow = r < BM / 2 ? stage_lo + r * EP : stage_hi + (r - BM / 2) * EP;
+        const int m = m0 + r;
+        const float sxm = I8 && m < p.M ? p.sx[m] : 0.0f;
+        if constexpr (I8) {
+          // the raw int32 accumulators, when asked for (bit-exact checks)
+          if (p.acc_out != nullptr && m < p.M) {
+            int32_t* arow = p.acc_out + (size_t)m * p.N;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const int n = n0 + wn * WTN + j * 32 + g * 8 + lcol;
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                if (n + t < p.N) { arow[n + t] = acc[i][j][4 * g + t]; }
+              }
+            }
+          }
+        }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           float v[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            v[t] = acc[i][j][4 * g + t] + bv[g][t];
-            if (p.epilogue == kEpiGelu) { v[t] = gelu_tanh(v[t]); }
+            if constexpr (I8) {
+              // y = bf16(fma(float(acc), sx[m] * sw[n], bias[n])), that order
+              v[t] = fmaf((float)acc[i][j][4 * g + t], sxm * swv[g][t], bv[g][t]);
+            } else {
+              v[t] = acc[i][j][4 * g + t] + bv[g][t];
+              if (p.epilogue == kEpiGelu) { v[t] = gelu_tanh(v[t]); }
+            }
           }
           *(uint2*)(srow + wn * WTN + j * 32 + g * 8 + lcol) =
               make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
@@ -566,10 +608,45 @@ GemmPlan plan_gemm(int M, int N, int K, int cu_count)
   return plan;
 }
 
+hipError_t launch_i8_gemm(const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
+                          const void* bias, int bias_type, uint16_t* y, int32_t* acc, int M,
+                          int K, int N, hipStream_t stream)
+{
+  KParams kp = {};
+  kp.xq = xq;
+  kp.sx = sx;
+  kp.sw = sw;
+  kp.acc_out = acc;
+  kp.wq = (const uint8_t*)wq;
+  kp.bias = bias;
+  kp.bias_type = bias != nullptr ? bias_type : kBiasNone;
+  kp.epilogue = kEpiNone;
+  kp.y = y;
+  kp.M = M;
+  kp.N = N;
+  kp.K = K;
+  kp.k_chunk = K;
+  int dev = 0;
+  int cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    cus = 256;
+  }
+  // the tall tile when it fills the GPU, else 128 x 128
+  if ((long)((M + 255) / 256) * ((N + 255) / 256) >= cus) {
+    kp.tiles_m = (M + 255) / 256;
+    kp.tiles_n = (N + 255) / 256;
+    return launch_cfg<256, 256, kTallWM, kTallWN, kI8Ops, false>(kp, 1, stream);
+  }
+  kp.tiles_m = (M + 127) / 128;
+  kp.tiles_n = (N + 127) / 128;
+  return launch_cfg<128, 128, 2, 2, kI8Ops, false>(kp, 1, stream);
+}
+
 hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
                        float* workspace, hipStream_t stream)
 {
-  KParams kp;
+  KParams kp = {};
   kp.x = d.x;
   kp.wq = (const uint8_t*)d.w;
   kp.wd = (const uint16_t*)d.w;
