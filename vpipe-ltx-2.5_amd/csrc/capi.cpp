@@ -67,8 +67,6 @@ struct DeviceState {
   char arch[64] = {0};
   void* ws = nullptr;        // split-K f32 partials
   size_t ws_bytes = 0;
-  void* cnt = nullptr;       // skinny split-K arrival counters, kept zero
-  size_t cnt_bytes = 0;
   void* i8 = nullptr;        // int8 tier operands: xq | sx | wq | sw
   size_t i8_bytes = 0;
   void* deq = nullptr;       // dequant-once arm: bf16 [N][K] expansion
@@ -135,17 +133,6 @@ int grow(void** buf, size_t* cap, size_t need)
   }
   *cap = need;
   return LTX25_OK;
-}
-
-// Grow a buffer whose contents must start at zero (the skinny path's
-// arrival counters; its kernels return every counter to zero).
-int grow_zeroed(void** buf, size_t* cap, size_t need)
-{
-  if (*cap >= need) { return LTX25_OK; }
-  const int rc = grow(buf, cap, need);
-  if (rc != LTX25_OK) { return rc; }
-  const hipError_t e = hipMemset(*buf, 0, *cap);
-  return e == hipSuccess ? LTX25_OK : hip_fail(e, "hipMemset (counters)");
 }
 
 // The kernels move 16-byte vectors, so every tensor base must be 16-byte
@@ -263,23 +250,6 @@ int run_linear(hipStream_t st, const void* x, const ltx25_qweight* w,
   d.M = M;
   d.N = N;
   d.K = K;
-  if (M <= ltx25::kSkinnyMaxM) {
-    const ltx25::SkinnyPlan sp = ltx25::plan_skinny(M, N, K, ds->cu_count);
-    float* part = nullptr;
-    int* cnt = nullptr;
-    if (sp.splits > 1) {
-      std::lock_guard<std::mutex> lk(g_mu);
-      rc = grow(&ds->ws, &ds->ws_bytes, sp.workspace_bytes);
-      if (rc != LTX25_OK) { return rc; }
-      rc = grow_zeroed(&ds->cnt, &ds->cnt_bytes, (size_t)sp.counter_count * sizeof(int));
-      if (rc != LTX25_OK) { return rc; }
-      part = (float*)ds->ws;
-      cnt = (int*)ds->cnt;
-    }
-    const hipError_t e = ltx25::launch_skinny(d, sp, part, cnt, st);
-    if (e != hipSuccess) { return hip_fail(e, "skinny qgemm launch"); }
-    return LTX25_OK;
-  }
   const ltx25::GemmPlan plan = ltx25::plan_gemm(M, N, K, ds->cu_count);
   float* ws = nullptr;
   if (plan.workspace_bytes > 0) {

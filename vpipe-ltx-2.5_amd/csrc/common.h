@@ -118,24 +118,6 @@ GemmPlan plan_gemm(int M, int N, int K, int cu_count);
 hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
                        float* workspace, hipStream_t stream);
 
-// The skinny path (M <= kSkinnyMaxM): one workgroup per 32*waves columns
-// and K split; f32 partials and one zero-initialised counter per column
-// tile when splits > 1. Not yet routed (kSkinnyMaxM = 0): at the audio
-// shapes it is still slower than the 128 x 128 split-K tile.
-constexpr int kSkinnyMaxM = 0;
-struct SkinnyPlan {
-  int waves = 4;
-  int splits = 1;
-  int k_chunk = 0;
-  int tiles_n = 0;
-  size_t workspace_bytes = 0;   // f32 partials [splits][M][N]
-  int counter_count = 0;        // ints, zero between launches
-};
-
-SkinnyPlan plan_skinny(int M, int N, int K, int cu_count);
-hipError_t launch_skinny(const GemmDesc& d, const SkinnyPlan& plan, float* partial,
-                         int* counters, hipStream_t stream);
-
 // The low-rank adapter delta y += (x . A^T) . B^T (lora.hip). One launch
 // covers at most kLoraMaxRank adapter columns: `a` points at the pass's
 // first row of A [rank][K], `b` at its first column of B [N][ldb]. `vec`

@@ -40,6 +40,9 @@ namespace {
 // Wave grid of the 256 x 256 tile.
 constexpr int kTallWM = 2;
 constexpr int kTallWN = 4;
+// Width of the small tile (128 rows; four waves, 2 x 2 at 128 columns or
+// 4 x 1 at 64).
+constexpr int kSkinnyBN = 128;
 constexpr int kBK = 64;             // K per main-loop step (bf16 activations)
 // BITS value of the int8 x int8 -> int32 GEMM (the int8 tier): both
 // operands are int8 rows, 128 of K per step in the same 128-byte LDS rows.
@@ -565,8 +568,14 @@ hipError_t launch_tile(const KParams& kp, int bits, int splits,
       return split ? launch_cfg<BM, BN, WM, WN, 8, true>(kp, splits, stream)
                    : launch_cfg<BM, BN, WM, WN, 8, false>(kp, splits, stream);
     case 4:
-      return split ? launch_cfg<BM, BN, WM, WN, 4, true>(kp, splits, stream)
-                   : launch_cfg<BM, BN, WM, WN, 4, false>(kp, splits, stream);
+      // 32 w4 codes per 16-byte chunk: a tile narrower than 128 columns
+      // has fewer chunks per step than threads
+      if constexpr (BN * kBK * 4 / 8 / 16 >= WM * WN * 64) {
+        return split ? launch_cfg<BM, BN, WM, WN, 4, true>(kp, splits, stream)
+                     : launch_cfg<BM, BN, WM, WN, 4, false>(kp, splits, stream);
+      } else {
+        return hipErrorInvalidValue;
+      }
     default:
       return split ? launch_cfg<BM, BN, WM, WN, 16, true>(kp, splits, stream)
                    : launch_cfg<BM, BN, WM, WN, 16, false>(kp, splits, stream);
@@ -593,7 +602,7 @@ GemmPlan plan_gemm(int M, int N, int K, int cu_count)
     return plan;
   }
   plan.tile = 1;
-  const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
+  const long tiles = (long)((M + 127) / 128) * ((N + kSkinnyBN - 1) / kSkinnyBN);
   const long want = (2L * cu_count + tiles - 1) / tiles;
   // At least 512 of K per split: each split writes a full f32 partial of
   // the output, which at the audio shapes outweighs the weights themselves
@@ -664,13 +673,14 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
   kp.bias_type = d.bias != nullptr ? d.bias_type : kBiasNone;
   kp.epilogue = d.epilogue;
   const int bm = plan.tile == 0 ? 256 : 128;
-  const int bn = plan.tile == 0 ? 256 : 128;
+  const int bn = plan.tile == 0 ? 256 : kSkinnyBN;
   kp.tiles_m = (d.M + bm - 1) / bm;
   kp.tiles_n = (d.N + bn - 1) / bn;
 
   hipError_t e = plan.tile == 0
                      ? launch_tile<256, 256, kTallWM, kTallWN>(kp, d.bits, plan.splits, stream)
-                     : launch_tile<128, 128, 2, 2>(kp, d.bits, plan.splits, stream);
+                     : launch_tile<128, kSkinnyBN, 2 * 128 / kSkinnyBN, kSkinnyBN / 64>(
+                           kp, d.bits, plan.splits, stream);
   if (e != hipSuccess || plan.splits <= 1) { return e; }
   const size_t total = (size_t)d.M * d.N;
   const unsigned blocks = (unsigned)((total + 1023) / 1024);
