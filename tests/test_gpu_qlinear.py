@@ -273,6 +273,42 @@ def test_config2_video_ffn_pair(pkg):
     check_full_vs_torch(y, h, d2)
 
 
+# One joint audio-video block's linear set (config 4), at the real token counts: video 8160,
+# audio 126, text 1024. Fused QKV (N = 3 x inner) and text K/V packs, f32 biases where the
+# block has them, GELU fused into both ff_in projections. The video launches take the
+# dequant-once route (M >= 4096), the text and audio ones the fused kernel.
+BLOCK4 = [
+    ("v_qkv", 8160, 4096, 12288, True, False), ("v_out", 8160, 4096, 4096, True, False),
+    ("v_xkv", 1024, 4096, 8192, True, False), ("v_ff_up", 8160, 4096, 16384, False, True),
+    ("v_ff_down", 8160, 16384, 4096, False, False), ("a_qkv", 126, 2048, 6144, True, False),
+    ("a_xkv", 1024, 2048, 4096, True, False), ("a_ff_up", 126, 2048, 8192, True, True),
+    ("a_ff_down", 126, 8192, 2048, True, False), ("a2v_q", 8160, 4096, 2048, True, False),
+    ("a2v_o", 8160, 2048, 4096, True, False), ("v2a_kv", 8160, 4096, 4096, True, False),
+]
+
+
+@pytest.mark.parametrize("name,M,K,N,has_bias,gelu", BLOCK4, ids=[b[0] for b in BLOCK4])
+def test_config4_block_linear_set(pkg, name, M, K, N, has_bias, gelu):
+    say(f"config 4: {name} {M}x{K}->{N} bias={has_bias} gelu={gelu}")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(40 + len(name) * 7 + N)
+    x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), device="cuda", generator=g) * 0.02
+    codes = torch.empty((N, K), dtype=torch.uint8, device="cuda")
+    sc = torch.empty((N, K // 64), dtype=torch.bfloat16, device="cuda")
+    qb = torch.empty((N, K // 64), dtype=torch.bfloat16, device="cuda")
+    pkg.quantize_affine(w, codes, sc, qb, N, K, 8, 64)
+    q = pkg.QWeight(codes, sc, qb, 8, 64)
+    deq = torch.empty((N, K), dtype=torch.bfloat16, device="cuda")
+    pkg.dequant(q, deq, N, K)
+    b = (torch.randn((N,), device="cuda", generator=g) * 0.01) if has_bias else None
+    y = run_q(pkg, x, q, b, M, K, N, pkg.EPI_GELU_TANH if gelu else pkg.EPI_NONE)
+    bias_h = host_f32(b) if has_bias else None
+    check_rows_vs_oracle(y, host_f32(x), host_f32(deq), bias_h, sample_rows(M, 6),
+                         epilogue="gelu" if gelu else None)
+    check_full_vs_torch(y, x, deq, b, gelu=gelu)
+
+
 def test_gelu_epilogue_matches_separate_gelu(pkg):
     say("fused GELU epilogue vs linear then gelu")
     M, K, N = 300, 512, 640
