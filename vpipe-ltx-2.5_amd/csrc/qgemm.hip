@@ -127,7 +127,7 @@ __device__ __forceinline__ void interleave()
   interleave_seq<NM, NR, NW, NV, NG>(std::make_integer_sequence<int, NM>{});
 }
 
-template <int BM, int BN, int WM, int WN, int BITS, bool SPLIT>
+template <int BM, int BN, int WM, int WN, int BITS, bool SPLIT, int NS = 0>
 __global__ void __launch_bounds__(WM * WN * 64)
 qgemm_kernel(KParams p)
 {
@@ -343,7 +343,7 @@ qgemm_kernel(KParams p)
   constexpr int kB1 = B_LD / 2;
   constexpr int kValuChunk = !QUANT ? 0 : (BITS == 8 ? 42 : 86);
   constexpr int kWrChunk = !QUANT ? 1 : (BITS == 8 ? 2 : 4);
-  auto step = [&](int s, auto do_store, auto do_load) {
+  auto step = [&](int s, auto do_store, auto do_load, int ld) {
     constexpr bool kStore = decltype(do_store)::value;
     constexpr bool kLoad = decltype(do_load)::value;
     constexpr int kGlB = QUANT ? 3 * B_LD : B_LD;
@@ -357,14 +357,14 @@ qgemm_kernel(KParams p)
     read_frags(st, 2, 0);
     mfma_all(1);
     if constexpr (kStore) { store_b_rows(nst, 0, kB1); }
-    if constexpr (kLoad) { load_a(kbeg + (s + 2) * SK); }
+    if constexpr (kLoad) { load_a(kbeg + ld * SK); }
     interleave<kMf, kRd, kStore ? kB1 * kWrChunk : 0, kStore ? kB1 * kValuChunk : 0,
                kLoad ? A_LD : 0>();
     __builtin_amdgcn_sched_barrier(0);
     read_frags(st, 3, 1);
     mfma_all(0);
     if constexpr (kStore) { store_b_rows(nst, kB1, B_LD); }
-    if constexpr (kLoad) { load_b(kbeg + (s + 2) * SK); }
+    if constexpr (kLoad) { load_b(kbeg + ld * SK); }
     interleave<kMf, kRd, kStore ? (B_LD - kB1) * kWrChunk : 0,
                kStore ? (B_LD - kB1) * kValuChunk : 0, kLoad ? kGlB : 0>();
     __builtin_amdgcn_sched_barrier(0);
@@ -375,7 +375,60 @@ qgemm_kernel(KParams p)
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  if (nsteps > 0) {
+  if constexpr (NS > 0) {
+    // A split-K slice of exactly NS steps, fully unrolled, with the loads
+    // kRing steps ahead of their LDS store (a register ring of kRing slots)
+    // instead of one: under load a dependent memory round trip costs about
+    // as much as five steps of this tile's MFMAs, so a one-step lookahead
+    // stalls every other step. Step t lives in slot t % kRing.
+    constexpr int kRing = 4;
+    uint4 ar[kRing][A_LD];
+    uint4 br[kRing][B_LD];
+    uint16_t sr[kRing][B_LD];
+    uint16_t qr[kRing][B_LD];
+    auto to_slot = [&](int t) {
+#pragma unroll
+      for (int i = 0; i < A_LD; ++i) { ar[t % kRing][i] = areg[i]; }
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i) {
+        br[t % kRing][i] = breg[i];
+        sr[t % kRing][i] = sraw[i];
+        qr[t % kRing][i] = qraw[i];
+      }
+    };
+    auto from_slot = [&](int t) {
+#pragma unroll
+      for (int i = 0; i < A_LD; ++i) { areg[i] = ar[t % kRing][i]; }
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i) {
+        breg[i] = br[t % kRing][i];
+        sraw[i] = sr[t % kRing][i];
+        qraw[i] = qr[t % kRing][i];
+      }
+    };
+    load_regs(kbeg);
+    store_a(0);
+    store_b(0);
+#pragma unroll
+    for (int t = 1; t <= kRing && t < NS; ++t) {
+      load_regs(kbeg + t * SK);
+      to_slot(t);
+    }
+    __syncthreads();
+    read_frags(0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      if (t + 1 < NS) { from_slot(t + 1); }
+      if (t + 1 < NS && t + 1 + kRing < NS) {
+        step(t, std::true_type{}, std::true_type{}, t + 1 + kRing);
+        to_slot(t + 1 + kRing);
+      } else if (t + 1 < NS) {
+        step(t, std::true_type{}, std::false_type{}, 0);
+      } else {
+        step(t, std::false_type{}, std::false_type{}, 0);
+      }
+    }
+  } else if (nsteps > 0) {
     // Two LDS stages; the last two steps are peeled so that the
     // steady-state body has no branches.
     load_regs(kbeg);
@@ -385,12 +438,12 @@ qgemm_kernel(KParams p)
     __syncthreads();
     read_frags(0, 0, 0);
     int s = 0;
-    for (; s + 2 < nsteps; ++s) { step(s, std::true_type{}, std::true_type{}); }
+    for (; s + 2 < nsteps; ++s) { step(s, std::true_type{}, std::true_type{}, s + 2); }
     if (s + 1 < nsteps) {
-      step(s, std::true_type{}, std::false_type{});
+      step(s, std::true_type{}, std::false_type{}, 0);
       ++s;
     }
-    step(s, std::false_type{}, std::false_type{});
+    step(s, std::false_type{}, std::false_type{}, 0);
   }
 
   // Accumulator layout. The MFMAs take the weight fragment as their first
@@ -549,10 +602,20 @@ splitk_reduce_kernel(const float* partial, int splits, const void* bias,
   }
 }
 
+// Steps of the fully unrolled split-K slice (the audio shapes' K / 512).
+constexpr int kSplitSteps = 8;
+
 template <int BM, int BN, int WM, int WN, int BITS, bool SPLIT>
 hipError_t launch_cfg(const KParams& kp, int splits, hipStream_t stream)
 {
   const dim3 grid((unsigned)(kp.tiles_m * kp.tiles_n), (unsigned)splits, 1);
+  if constexpr (SPLIT && BITS != kI8Ops && BM == 128) {
+    if (kp.k_chunk == kSplitSteps * kBK && kp.K % kp.k_chunk == 0) {
+      hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, BITS, SPLIT, kSplitSteps>), grid,
+                         dim3(WM * WN * 64), 0, stream, kp);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, BITS, SPLIT>), grid,
                      dim3(WM * WN * 64), 0, stream, kp);
   return hipGetLastError();
