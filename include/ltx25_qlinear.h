@@ -166,14 +166,20 @@ int ltx25_dequant_once_takes(int M, int K, int N);
 
 /* y[M][N] += (x[M][K] . a[rank][K]^T) . b[N][rank]^T, all bf16, in place on
  * y: r = bf16(x . a^T) with f32 accumulation, then y = bf16(f32(y) + r . b^T)
- * with the accumulator seeded from y. One fused kernel per 512 adapter
- * columns; `r` ([M][rank]) and `d` ([M][N]) are the reference signature's
- * caller scratch and are neither read nor written (either may be NULL).
- * An empty shape (any of M, K, N, rank <= 0) is a no-op, as in the
- * reference. Pointers need only bf16 (2-byte) alignment; 16-byte aligned
- * x, a and y with K % 8 == 0 and N % 8 == 0 take the vector path (when the
- * rank is not a multiple of 8, b is first copied with its rows zero-padded
- * to one, into a grow-only scratch).
+ * with the accumulator seeded from y. Two routes, same arithmetic:
+ * - rank >= 96, M >= 256, K % 64 == 0, N % 8 == 0, 16-byte aligned x and y:
+ *   the reference's matrix-core pair -- r on the dense GEMM, then the dense
+ *   GEMM again with its accumulators seeded from y; the rank is padded to a
+ *   multiple of 64 (a and b copied with zero rows / columns when needed) in
+ *   a grow-only scratch that also holds r;
+ * - otherwise one fused kernel per 512 adapter columns (16-byte aligned x,
+ *   a and y with K % 8 == 0 and N % 8 == 0 take its vector path; when the
+ *   rank is not a multiple of 8, b is first copied with its rows
+ *   zero-padded to one).
+ * `r` ([M][rank]) and `d` ([M][N]) are the reference signature's caller
+ * scratch and are neither read nor written (either may be NULL). An empty
+ * shape (any of M, K, N, rank <= 0) is a no-op, as in the reference.
+ * Pointers need only bf16 (2-byte) alignment.
  * Replaces MetalOps::lora_add (src/ltx25-metal-ops.h:107-133;
  * src/ltx25-metal-ops.cc:989-1004) and its matrix-core pair (:940-987). */
 int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,

@@ -39,6 +39,11 @@ SHAPES = [
     ("two launches (rank 600)", 70, 256, 192, 600),
     ("two launches, padded rank (530)", 96, 256, 320, 530),
     ("N not a multiple of 8 (element-wise y)", 40, 128, 4100, 16),
+    # the GEMM pair (M >= 256, rank >= 64): rank padded to 64 with zero rows / columns
+    ("GEMM pair, rank 128, no padding", 300, 2048, 1024, 128),
+    ("GEMM pair, rank 450 padded to 512", 512, 1024, 2048, 450),
+    ("GEMM pair, ragged M and N", 777, 512, 1000, 200),
+    ("GEMM pair, rank 1000 (split-K second GEMM)", 256, 512, 640, 1000),
 ]
 
 

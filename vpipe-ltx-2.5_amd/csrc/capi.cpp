@@ -73,6 +73,8 @@ struct DeviceState {
   size_t deq_bytes = 0;
   void* lora_b = nullptr;    // LoRA B padded to a multiple of 8 columns
   size_t lora_b_bytes = 0;
+  void* lora_mm = nullptr;   // LoRA GEMM pair: A padded | r | B padded
+  size_t lora_mm_bytes = 0;
 };
 
 std::mutex g_mu;
@@ -304,6 +306,89 @@ int run_i8_linear(DeviceState* ds, hipStream_t st, const void* x,
   return LTX25_OK;
 }
 
+// The LoRA delta as the reference's matrix-core pair (lora_mma_,
+// src/ltx25-metal-ops.cc:938-987): r = bf16(x . A^T) on the dense GEMM, then
+// y = bf16(y + r . B^T) on the dense GEMM with its accumulate epilogue. The
+// rank is padded to a multiple of 64 (A's extra rows and B's extra columns
+// zero, so r's extra columns are zero and add nothing). Taken from rank
+// kLoraPairMinRank up, where the adapter's FLOPs outweigh re-reading y:
+// below it the fused one-pass kernel, bound by y's traffic, is faster.
+constexpr int kLoraPairMinRank = 96;
+
+bool lora_pair_takes(int M, int K, int N, int rank, const void* x, const void* y)
+{
+  const size_t two_gib = (size_t)1 << 31;
+  const size_t rk = (size_t)((rank + 63) & ~63);
+  return rank >= kLoraPairMinRank && M >= 256 && K % 64 == 0 && N % 8 == 0 &&
+         aligned16(x) && aligned16(y) && (size_t)M * K * 2 < two_gib &&
+         (size_t)M * N * 2 < two_gib && rk * K * 2 < two_gib && (size_t)N * rk * 2 < two_gib &&
+         (size_t)M * rk * 2 < two_gib;
+}
+
+int lora_pair(DeviceState* ds, hipStream_t st, const void* x, const void* a, const void* b,
+              void* y, int M, int K, int N, int rank)
+{
+  const int rk = (rank + 63) & ~63;
+  const bool pad_a = rk != rank || !aligned16(a);
+  const bool pad_b = rk != rank || !aligned16(b);
+  const size_t a_bytes = pad_a ? align256((size_t)rk * K * 2) : 0;
+  const size_t r_bytes = align256((size_t)M * rk * 2);
+  const size_t b_bytes = pad_b ? align256((size_t)N * rk * 2) : 0;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const int rc = grow(&ds->lora_mm, &ds->lora_mm_bytes, a_bytes + r_bytes + b_bytes);
+    if (rc != LTX25_OK) { return rc; }
+  }
+  char* base = (char*)ds->lora_mm;
+  const uint16_t* pa = (const uint16_t*)a;
+  uint16_t* pr = (uint16_t*)(base + a_bytes);
+  const uint16_t* pb = (const uint16_t*)b;
+  if (pad_a) {
+    // A [rank][K] -> [rk][K]: one row of rank*K elements, zero-filled to rk*K
+    const hipError_t e = ltx25::launch_lora_pad(pa, 1, rank * K, rank * K, (uint16_t*)base,
+                                                rk * K, st);
+    if (e != hipSuccess) { return hip_fail(e, "lora pad launch"); }
+    pa = (const uint16_t*)base;
+  }
+  if (pad_b) {
+    uint16_t* dst = (uint16_t*)(base + a_bytes + r_bytes);
+    const hipError_t e = ltx25::launch_lora_pad(pb, N, rank, rank, dst, rk, st);
+    if (e != hipSuccess) { return hip_fail(e, "lora pad launch"); }
+    pb = dst;
+  }
+  for (int half = 0; half < 2; ++half) {
+    ltx25::GemmDesc d;
+    d.bits = 16;
+    d.group = 64;
+    d.M = M;
+    if (half == 0) {
+      d.x = (const uint16_t*)x;
+      d.w = pa;
+      d.y = pr;
+      d.N = rk;
+      d.K = K;
+    } else {
+      d.x = pr;
+      d.w = pb;
+      d.y = (uint16_t*)y;
+      d.y_in = (const uint16_t*)y;
+      d.N = N;
+      d.K = rk;
+    }
+    const ltx25::GemmPlan plan = ltx25::plan_gemm(d.M, d.N, d.K, ds->cu_count);
+    float* ws = nullptr;
+    if (plan.workspace_bytes > 0) {
+      std::lock_guard<std::mutex> lk(g_mu);
+      const int rc = grow(&ds->ws, &ds->ws_bytes, plan.workspace_bytes);
+      if (rc != LTX25_OK) { return rc; }
+      ws = (float*)ds->ws;
+    }
+    const hipError_t e = ltx25::launch_gemm(d, plan, ws, st);
+    if (e != hipSuccess) { return hip_fail(e, "lora gemm launch"); }
+  }
+  return LTX25_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -443,6 +528,9 @@ int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
   DeviceState* ds = nullptr;
   const int rc = current_device(&ds);
   if (rc != LTX25_OK) { return rc; }
+  if (lora_pair_takes(M, K, N, rank, x, y)) {
+    return lora_pair(ds, (hipStream_t)stream, x, a, b, y, M, K, N, rank);
+  }
   // The vector path: 16-byte operand loads and 32-bit buffer offsets. B is
   // copied with its rank padded to a multiple of 8 when it is not already.
   const int rank8 = (rank + 7) & ~7;

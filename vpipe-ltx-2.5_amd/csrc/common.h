@@ -103,6 +103,7 @@ struct GemmDesc {
   int bias_type = kBiasNone;
   int epilogue = kEpiNone;
   uint16_t* y = nullptr;
+  const uint16_t* y_in = nullptr;   // when set: y = bf16(acc + bias + y_in), y_in may be y
   int M = 0, N = 0, K = 0;
 };
 

@@ -352,16 +352,33 @@ hipError_t launch_rb(const LoraParams& p, bool vec, dim3 grid, hipStream_t strea
   return hipGetLastError();
 }
 
-// dst[r][c] = c < cols ? src[r][c] : 0 for c < ld_dst: B with its rank
-// padded to a multiple of 8 columns, so the vector path can load it.
+// dst[r][c] = c < cols ? src[r][c] : 0 for c < ld_dst (ld_dst % 8 == 0): an
+// adapter matrix with its rank padded, so the vector paths can load it. One
+// thread per 8 destination elements (one 16-byte store); the source side
+// reads 16 bytes at once when its row start and stride allow it.
 __global__ void lora_pad_kernel(const uint16_t* __restrict__ src, int rows, int cols,
                                 int ld_src, uint16_t* __restrict__ dst, int ld_dst)
 {
+  const size_t chunks = (size_t)ld_dst / 8;
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (size_t)rows * ld_dst) { return; }
-  const int r = (int)(i / ld_dst);
-  const int c = (int)(i % ld_dst);
-  dst[i] = c < cols ? src[(size_t)r * ld_src + c] : (uint16_t)0;
+  if (i >= (size_t)rows * chunks) { return; }
+  const size_t r = i / chunks;
+  const int c = (int)(i % chunks) * 8;
+  const uint16_t* s = src + r * (size_t)ld_src + c;
+  uint4 v;
+  if (c + 8 <= cols && ((uintptr_t)s & 15u) == 0) {
+    v = *(const uint4*)s;
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t lo = c + 2 * t < cols ? s[2 * t] : 0u;
+      const uint32_t hi = c + 2 * t + 1 < cols ? s[2 * t + 1] : 0u;
+      w[t] = lo | (hi << 16);
+    }
+    v = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  *(uint4*)(dst + r * (size_t)ld_dst + c) = v;
 }
 
 }  // namespace
@@ -369,7 +386,8 @@ __global__ void lora_pad_kernel(const uint16_t* __restrict__ src, int rows, int 
 hipError_t launch_lora_pad(const uint16_t* src, int rows, int cols, int ld_src, uint16_t* dst,
                            int ld_dst, hipStream_t stream)
 {
-  const size_t n = (size_t)rows * ld_dst;
+  if (ld_dst % 8 != 0 || ((uintptr_t)dst & 15u) != 0) { return hipErrorInvalidValue; }
+  const size_t n = (size_t)rows * (ld_dst / 8);
   if (n == 0) { return hipSuccess; }
   lora_pad_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(src, rows, cols, ld_src, dst,
                                                                      ld_dst);

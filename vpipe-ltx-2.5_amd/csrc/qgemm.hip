@@ -62,6 +62,7 @@ struct KParams {
   const uint16_t* qbias;
   const void* bias;
   uint16_t* y;
+  const uint16_t* y_in;    // accumulate source (may alias y), or null
   float* partial;          // [splits][M][N] when split
   int M, N, K;
   int gshift;              // log2(group)
@@ -286,6 +287,42 @@ qgemm_kernel(KParams p)
       for (int r = 0; r < 16; ++r) { acc[i][j][r] = 0; }
     }
   }
+  // Accumulate into an existing output (the LoRA delta's second GEMM): the
+  // accumulators start from y_in, in the MFMA layout (block (i, j), lane l,
+  // registers 4g..4g+3: row 32 i + l % 32, four consecutive columns from
+  // 32 j + 8 g + 4 (l / 32)), so the K loop adds the products to it and the
+  // epilogue rounds once. These loads overlap the operand prologue's.
+  if constexpr (!I8 && !SPLIT) {
+    if (p.y_in != nullptr) {
+      const int lrow0 = lane & 31;
+      const int lcol0 = (lane >> 5) * 4;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int m = m0 + wm * (BM / WM) + i * 32 + lrow0;
+        if (m >= p.M) { continue; }
+        const uint16_t* yrow = p.y_in + (size_t)m * p.N;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int n = n0 + wn * (BN / WN) + j * 32 + g * 8 + lcol0;
+            if ((p.N & 3) == 0 && n + 3 < p.N) {
+              const uint2 o = *(const uint2*)(yrow + n);
+              acc[i][j][4 * g + 0] = __uint_as_float(o.x << 16);
+              acc[i][j][4 * g + 1] = __uint_as_float(o.x & 0xffff0000u);
+              acc[i][j][4 * g + 2] = __uint_as_float(o.y << 16);
+              acc[i][j][4 * g + 3] = __uint_as_float(o.y & 0xffff0000u);
+            } else {
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                acc[i][j][4 * g + t] = n + t < p.N ? bf16_to_f32(yrow[n + t]) : 0.0f;
+              }
+            }
+          }
+        }
+      }
+    }
+  }
 
   // Fragment registers, double-buffered across the four 16-deep K slices
   // of a step: slice kk+1 is read from LDS while slice kk's MFMAs run.
@@ -486,6 +523,8 @@ qgemm_kernel(KParams p)
                   "the staged output tile must fit the operand stages");
     uint16_t* const stage_lo = &lds_a[0][0];
     uint16_t* const stage_hi = &lds_b[0][0];
+    constexpr int CPR = BN / 8;   // 16-byte chunks per row
+    const bool vec_rows = (p.N & 7) == 0;
     __syncthreads();   // every wave is done reading the operand tiles
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
@@ -530,8 +569,11 @@ qgemm_kernel(KParams p)
               v[t] = fmaf((float)acc[i][j][4 * g + t], sxm * swv[g][t], bv[g][t]);
             } else {
               v[t] = acc[i][j][4 * g + t] + bv[g][t];
-              if (p.epilogue == kEpiGelu) { v[t] = gelu_tanh(v[t]); }
             }
+          }
+          if (!I8 && p.epilogue == kEpiGelu) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) { v[t] = gelu_tanh(v[t]); }
           }
           *(uint2*)(srow + wn * WTN + j * 32 + g * 8 + lcol) =
               make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
@@ -539,8 +581,6 @@ qgemm_kernel(KParams p)
       }
     }
     __syncthreads();
-    constexpr int CPR = BN / 8;   // 16-byte chunks per row
-    const bool vec_rows = (p.N & 7) == 0;
 #pragma unroll 4
     for (int q = tid; q < BM * CPR; q += NT) {
       const int r = q / CPR;
@@ -569,7 +609,8 @@ qgemm_kernel(KParams p)
 // Sum the split-K partials in split order, then bias, epilogue, bf16.
 __global__ void __launch_bounds__(256)
 splitk_reduce_kernel(const float* partial, int splits, const void* bias,
-                     int bias_type, int epilogue, uint16_t* y, int M, int N)
+                     int bias_type, int epilogue, const uint16_t* y_in, uint16_t* y, int M,
+                     int N)
 {
   const size_t total = (size_t)M * N;
   const size_t i0 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
@@ -586,6 +627,7 @@ splitk_reduce_kernel(const float* partial, int splits, const void* bias,
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       float v = s[t] + load_bias(bias, bias_type, n + t);
+      if (y_in != nullptr) { v += bf16_to_f32(y_in[i0 + t]); }
       if (epilogue == kEpiGelu) { v = gelu_tanh(v); }
       o[t] = v;
     }
@@ -597,6 +639,7 @@ splitk_reduce_kernel(const float* partial, int splits, const void* bias,
     float v = partial[i];
     for (int k = 1; k < splits; ++k) { v += partial[(size_t)k * plane + i]; }
     v += load_bias(bias, bias_type, (int)(i % (size_t)N));
+    if (y_in != nullptr) { v += bf16_to_f32(y_in[i]); }
     if (epilogue == kEpiGelu) { v = gelu_tanh(v); }
     y[i] = f32_to_bf16(v);
   }
@@ -726,6 +769,7 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
   kp.qbias = d.qbias;
   kp.bias = d.bias;
   kp.y = d.y;
+  kp.y_in = d.y_in;
   kp.partial = workspace;
   kp.M = d.M;
   kp.N = d.N;
@@ -749,7 +793,7 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
   const unsigned blocks = (unsigned)((total + 1023) / 1024);
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream,
                      (const float*)workspace, plan.splits, kp.bias,
-                     kp.bias_type, d.epilogue, d.y, d.M, d.N);
+                     kp.bias_type, d.epilogue, d.y_in, d.y, d.M, d.N);
   return hipGetLastError();
 }
 
