@@ -538,6 +538,59 @@ def pmc_summary(fetch_csv, write_csv, cmd):
     print("\n".join(lines))
 
 
+def busy_summary(csv_path, out, cmd):
+    """Shader clock, MFMA-busy and L2-busy per kernel from one rocprofv3 --pmc
+    run with GRBM_GUI_ACTIVE, SQ_VALU_MFMA_BUSY_CYCLES and TCC_BUSY_avr.
+    GRBM_GUI_ACTIVE counts the graphics engine's active cycles summed over
+    the 8 XCDs, so /8 / duration is the clock; SQ_VALU_MFMA_BUSY_CYCLES sums
+    the busy cycles of every SIMD (32 per v_mfma_f32_32x32x16_bf16), so
+    dividing by the SIMD count (4 per CU) x the active cycles gives the
+    fraction of the elapsed time the matrix cores ran; TCC_BUSY_avr is the
+    mean busy cycles of an L2 channel."""
+    import csv
+
+    xcds, simds = 8, 4 * 256
+    per = {}
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            if "ltx25::" not in name:
+                continue
+            short = name[name.index("ltx25::"):].replace("(anonymous namespace)::", "")
+            short = short.split("(")[0]
+            key = (short, int(r["Grid_Size"]))
+            d = per.setdefault(key, {"dur": {}, "c": {}})
+            i = int(r["Dispatch_Id"])
+            d["dur"][i] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            d["c"].setdefault(r["Counter_Name"], {})[i] = float(r["Counter_Value"])
+    lines = ["# Clock, MFMA-busy and L2-busy per kernel (rocprofv3 --pmc)", "", "Command:", "",
+             "```", cmd, "```", "",
+             f"clock = GRBM_GUI_ACTIVE / {xcds} XCDs / duration; MFMA busy = "
+             f"SQ_VALU_MFMA_BUSY_CYCLES / ({simds} SIMDs x active cycles); L2 busy = "
+             "TCC_BUSY_avr / active cycles. Durations are the profiled dispatches' own. The "
+             "ratios mean something only for dispatches of ~100 us and more: the counters of "
+             "a short one also cover its launch and drain (hence clocks above the 2.4 GHz "
+             "maximum).", "",
+             "| kernel | grid | launches | avg us | clock GHz | MFMA busy | L2 busy |",
+             "|---|---|---|---|---|---|---|"]
+    for (short, grid), d in sorted(per.items(), key=lambda kv: -sum(kv[1]["dur"].values())):
+        ids = sorted(d["dur"])
+        g = d["c"].get("GRBM_GUI_ACTIVE", {})
+        mb = d["c"].get("SQ_VALU_MFMA_BUSY_CYCLES", {})
+        tb = d["c"].get("TCC_BUSY_avr", {})
+        dur = sum(d["dur"][i] for i in ids) / len(ids)
+        cyc = sum(g.get(i, 0.0) for i in ids) / len(ids) / xcds
+        mf = sum(mb.get(i, 0.0) for i in ids) / len(ids)
+        l2 = sum(tb.get(i, 0.0) for i in ids) / len(ids)
+        clk = cyc / dur if dur else 0.0
+        lines.append(f"| `{short}` | {grid} | {len(ids)} | {dur / 1e3:.1f} | {clk:.2f} | "
+                     f"{mf / (simds * cyc) if cyc else 0:.2f} | {l2 / cyc if cyc else 0:.2f} |")
+    lines.append("")
+    with open(out, "w") as f:
+        f.write("\n".join(lines))
+    print("\n".join(lines))
+
+
 def kernel_summary(db, out, cmd, note):
     """rocprofv3 kernel-trace database -> a short markdown table (via rocpd2summary)."""
     import csv
@@ -582,7 +635,13 @@ def main():
                     help="summarise two rocprofv3 --pmc counter files into profiles/ and exit")
     ap.add_argument("--kernel-summary", nargs=4, metavar=("DB", "OUT_MD", "CMD", "NOTE"),
                     help="summarise a rocprofv3 --kernel-trace database into OUT_MD and exit")
+    ap.add_argument("--busy-summary", nargs=3, metavar=("CSV", "OUT_MD", "CMD"),
+                    help="summarise a rocprofv3 --pmc run of GRBM_GUI_ACTIVE, "
+                         "SQ_VALU_MFMA_BUSY_CYCLES and TCC_BUSY_avr into OUT_MD and exit")
     args = ap.parse_args()
+    if args.busy_summary:
+        busy_summary(*args.busy_summary)
+        return
     if args.kernel_summary:
         kernel_summary(*args.kernel_summary)
         return
