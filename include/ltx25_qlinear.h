@@ -130,6 +130,17 @@ int ltx25_bias_add(void* stream, void* y, const void* bias, int bias_dtype,
  * 1061-1070; CPU form src/ltx25-block-ref.cc:265-272). */
 int ltx25_gelu_tanh(void* stream, const void* x, void* y, size_t n);
 
+/* Per-head gating of an attention output, in place:
+ * y[t][h*head_dim + d] = bf16(f32(y) * 2 / (1 + exp(-f32(logits[t][h])))),
+ * y bf16 [tokens][heads*head_dim], logits bf16 [tokens][heads] (the
+ * to_gate_logits linear's output). Non-positive sizes are a no-op. The
+ * 16-byte path needs head_dim % 8 == 0 and a 16-byte aligned y.
+ * Replaces MetalOps::gate_heads (src/ltx25-metal-ops.cc:1089-1101) and the
+ * ltx_gate_heads kernel (src/ltx25-kernels.metal:85-103); CPU form
+ * src/ltx25-block-ref.cc:113-125. */
+int ltx25_gate_heads(void* stream, void* y, const void* logits, int heads, int tokens,
+                     int head_dim);
+
 /* Expand a quantized weight to bf16 [N][K]: w = bf16(fma(scale, q, qbias)).
  * Replaces the dequant-once arm, affine_dequant_w{4,8}g{32,64}
  * (src/ltx25-metal-ops.cc:467-502). */

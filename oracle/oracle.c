@@ -283,6 +283,25 @@ void orc_bias_add_bf16(uint16_t* y, const uint16_t* bias, int M, int N)
   }
 }
 
+/* Per-head gating of an attention output, in place on bf16 y [tokens]
+ * [heads * head_dim]: gate = 2 / (1 + exp(-logit)) in float, from the bf16
+ * logit of (token, head); y = bf16(float(y) * gate). Restates
+ * src/ltx25-kernels.metal:85-103 (ltx_gate_heads; storage rounding of y)
+ * with the gate expression of src/ltx25-block-ref.cc:123. */
+void orc_gate_heads(uint16_t* y, const uint16_t* logits, int heads, int tokens, int head_dim)
+{
+  for (int t = 0; t < tokens; ++t) {
+    for (int h = 0; h < heads; ++h) {
+      const float lg = orc_bf16_to_f32(logits[(size_t)t * heads + h]);
+      const float gate = 2.0f / (1.0f + expf(-lg));
+      uint16_t* row = y + ((size_t)t * heads + h) * head_dim;
+      for (int d = 0; d < head_dim; ++d) {
+        row[d] = orc_bf16_rne(orc_bf16_to_f32(row[d]) * gate);
+      }
+    }
+  }
+}
+
 /* The low-rank adapter delta y += (x . a^T) . b^T, in place on bf16 y,
  * following MetalOps::lora_add (src/ltx25-metal-ops.cc:989-1004) in its
  * matrix-core form (:940-987): r = x . a^T is written to a bf16 scratch

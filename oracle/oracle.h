@@ -28,6 +28,12 @@
  *                                    and bit-exact against the reference's
  *                                    stream_ff_ GELU (oracle/_ref)
  *   orc_bias_add_bf16                torch bf16 add of the same operands
+ *   orc_gate_heads                   bit-exact against the reference's own
+ *                                    attention_ gating (oracle/_ref, v = a
+ *                                    constant, identity out-projection);
+ *                                    float64 sigmoid within one bf16 ulp;
+ *                                    logit 0 is the identity, +-large
+ *                                    logits double / zero y
  *   orc_lora_add                     the reference test's own known answer
  *                                    (f64 over the unrounded draws, rel-L2
  *                                    < 2e-2), numpy float64 matmuls with the
@@ -76,6 +82,7 @@ void orc_linear_f64_d(const float* x, const float* w, const float* bias,
 void orc_linear_f32_omp(const float* x, const float* w, const float* bias,
                         int M, int K, int N, float* out, int threads);
 void orc_gelu_tanh(const float* in, float* out, size_t n);
+void orc_gate_heads(uint16_t* y, const uint16_t* logits, int heads, int tokens, int head_dim);
 void orc_bias_add_bf16(uint16_t* y, const uint16_t* bias, int M, int N);
 
 /* ---- low-rank adapter delta --------------------------------------------- */

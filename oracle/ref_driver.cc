@@ -75,4 +75,45 @@ void ref_ff_identity(const float* x, int rows, int cols, double eps,
   std::memcpy(out, s.x.v.data(), (std::size_t)rows * cols * sizeof(float));
 }
 
+// The reference's attention_ reduced to its per-head gate: q, k and v
+// weights zero, v's bias `v_b` [heads * head_dim], the gate logits' weight
+// zero and bias `gate_b` [heads], an identity out-projection. Every row's
+// softmax then weighs v_b alone, the gate logits are gate_b, and
+//   out[r][h * head_dim + d] = v_b[h * head_dim + d] * 2 / (1 + exp(-gate_b[h]))
+// as the reference evaluates it (src/ltx25-block-ref.cc:113-125).
+void ref_gate_identity(const float* v_b, const float* gate_b, int heads, int head_dim, int rows,
+                       float* out)
+{
+  const int inner = heads * head_dim;
+  const int qdim = 8;
+  ltx25::AttnWeights w;
+  w.heads = heads;
+  w.head_dim = head_dim;
+  auto zeros = [](int r, int c) {
+    ltx25::Mat m;
+    m.rows = r;
+    m.cols = c;
+    m.v.assign((std::size_t)r * c, 0.0f);
+    return m;
+  };
+  w.q_w = zeros(inner, qdim);
+  w.k_w = zeros(inner, qdim);
+  w.v_w = zeros(inner, qdim);
+  w.o_w = zeros(inner, inner);
+  for (int i = 0; i < inner; ++i) { w.o_w.v[(std::size_t)i * inner + i] = 1.0f; }
+  w.q_b.assign(inner, 0.0f);
+  w.k_b.assign(inner, 0.0f);
+  w.v_b.assign(v_b, v_b + inner);
+  w.o_b.assign(inner, 0.0f);
+  w.q_norm.assign(inner, 1.0f);
+  w.k_norm.assign(inner, 1.0f);
+  w.gate_w = zeros(heads, qdim);
+  w.gate_b.assign(gate_b, gate_b + heads);
+  const ltx25::Mat x = zeros(rows, qdim);
+  const ltx25::Mat ctx = zeros(1, qdim);
+  ltx25::Mat o;
+  ltx25::attention_(w, x, ctx, nullptr, nullptr, o);
+  std::memcpy(out, o.v.data(), (std::size_t)rows * inner * sizeof(float));
+}
+
 }  // extern "C"

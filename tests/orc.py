@@ -36,6 +36,7 @@ _SIGS = {
     "orc_linear_f32_omp": (None, [_vp, _vp, _vp, _i, _i, _i, _vp, _i]),
     "orc_gelu_tanh": (None, [_vp, _vp, _sz]),
     "orc_bias_add_bf16": (None, [_vp, _vp, _i, _i]),
+    "orc_gate_heads": (None, [_vp, _vp, _i, _i, _i]),
     "orc_lora_add": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i]),
     "orc_i8_quantize_rows": (None, [_vp, _i, _i, _vp, _vp]),
     "orc_i8_gemm_i32": (None, [_vp, _vp, _i, _i, _i, _vp]),
@@ -73,6 +74,8 @@ def ref():
         r.ref_rms_norm.restype = None
         r.ref_ff_identity.argtypes = [_vp, _i, _i, ctypes.c_double, _vp]
         r.ref_ff_identity.restype = None
+        r.ref_gate_identity.argtypes = [_vp, _vp, _i, _i, _i, _vp]
+        r.ref_gate_identity.restype = None
         _ref = r
     return _ref
 
@@ -195,6 +198,16 @@ def bias_add_bf16(y, bias) -> np.ndarray:
     bias = _c(bias, np.uint16)
     M, N = y.shape
     lib().orc_bias_add_bf16(_p(y), _p(bias), M, N)
+    return y
+
+
+def gate_heads(y_bf16, logits_bf16, heads: int, head_dim: int) -> np.ndarray:
+    """y [tokens][heads*head_dim] * 2 sigmoid(logits [tokens][heads]) on bf16 bit patterns."""
+    y = np.array(y_bf16, dtype=np.uint16, copy=True)
+    lg = _c(logits_bf16, np.uint16)
+    tokens = lg.shape[0]
+    assert y.shape == (tokens, heads * head_dim) and lg.shape == (tokens, heads)
+    lib().orc_gate_heads(_p(y), _p(lg), heads, tokens, head_dim)
     return y
 
 

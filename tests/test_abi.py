@@ -72,6 +72,9 @@ def test_validation_precedes_any_device_use(pkg, lib):
     assert lib.ltx25_i8_gemm(None, fake, fake, fake, fake, None, 0, fake, None, 64, 100,
                              64) == pkg.E_UNSUPPORTED
     assert lib.ltx25_pack_codes(None, fake, fake, 4, 6, 8) == pkg.E_INVAL  # 6 codes != words
+    assert lib.ltx25_gate_heads(None, None, fake, 2, 2, 8) == pkg.E_INVAL      # null y
+    assert lib.ltx25_gate_heads(None, fake + 1, fake, 2, 2, 8) == pkg.E_INVAL  # odd address
+    assert lib.ltx25_gate_heads(None, None, None, 0, 2, 8) == pkg.OK           # empty: no-op
 
 
 def test_dequant_once_and_lora_gates(pkg, lib):

@@ -244,6 +244,42 @@ def test_gelu_bit_exact_against_reference_stream_ff():
     assert np.array_equal(out, expect)
 
 
+@ref_only
+def test_gate_bit_exact_against_reference_attention_gating():
+    rng = np.random.default_rng(21)
+    r = orc.ref()
+    heads, head_dim, rows = 6, 16, 3
+    # bf16-representable inputs, so that the oracle's bf16 operands are the reference's floats
+    v_b = orc.bf16_to_f32(torch_bf16_bits(rng.standard_normal(heads * head_dim).astype(np.float32)))
+    g_b = orc.bf16_to_f32(torch_bf16_bits((rng.standard_normal(heads) * 4).astype(np.float32)))
+    out = np.empty((rows, heads * head_dim), np.float32)
+    r.ref_gate_identity(v_b.ctypes.data, g_b.ctypes.data, heads, head_dim, rows, out.ctypes.data)
+    y = np.tile(torch_bf16_bits(v_b), (rows, 1))
+    lg = np.tile(torch_bf16_bits(g_b), (rows, 1))
+    got = orc.gate_heads(y, lg, heads, head_dim)
+    assert np.array_equal(got, torch_bf16_bits(out))
+
+
+def test_gate_heads_closed_form_and_special_cases():
+    rng = np.random.default_rng(22)
+    tokens, heads, head_dim = 5, 4, 24
+    y = torch_bf16_bits(rng.standard_normal((tokens, heads * head_dim)).astype(np.float32))
+    lg_f = (rng.standard_normal((tokens, heads)) * 3).astype(np.float32)
+    lg = torch_bf16_bits(lg_f)
+    got = orc.bf16_to_f32(orc.gate_heads(y, lg, heads, head_dim)).astype(np.float64)
+    g64 = 2.0 / (1.0 + np.exp(-orc.bf16_to_f32(lg).astype(np.float64)))
+    want = orc.bf16_to_f32(y).astype(np.float64) * np.repeat(g64, head_dim, axis=1)
+    # one bf16 rounding of a float product: within half an ulp of bf16 (2^-9 relative) plus
+    # the float gate's own rounding
+    assert np.all(np.abs(got - want) <= np.abs(want) * (2.0 ** -8) + 1e-30)
+    # logit 0: gate exactly 1, y unchanged; +88: gate 2, y doubled exactly; -100: exp
+    # overflows, the gate is 0 and y becomes a signed zero
+    for val, expect in [(0.0, lambda v: v), (88.0, lambda v: 2 * v), (-100.0, lambda v: 0 * v)]:
+        lgc = torch_bf16_bits(np.full((tokens, heads), val, np.float32))
+        out = orc.bf16_to_f32(orc.gate_heads(y, lgc, heads, head_dim))
+        assert np.array_equal(out, expect(orc.bf16_to_f32(y)).astype(np.float32)), val
+
+
 # ---- int8 tier ------------------------------------------------------------------------
 def test_i8_quantize_rows_closed_form():
     rng = np.random.default_rng(10)

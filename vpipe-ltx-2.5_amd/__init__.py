@@ -73,6 +73,7 @@ SIGNATURES = {
     "ltx25_linear": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i]),
     "ltx25_bias_add": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "ltx25_gelu_tanh": (_i, [_vp, _vp, _vp, _sz]),
+    "ltx25_gate_heads": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "ltx25_dequant": (_i, [_vp, ctypes.POINTER(QWeightC), _vp, _i, _i]),
     "ltx25_set_dequant_once": (_i, [_i]),
     "ltx25_dequant_once_takes": (_i, [_i, _i, _i]),
@@ -192,6 +193,11 @@ def bias_add(y, bias, M: int, N: int, stream=None) -> None:
 
 def gelu_tanh(x, y, stream=None) -> None:
     check(load().ltx25_gelu_tanh(_stream(stream), _ptr(x), _ptr(y), x.numel()))
+
+
+def gate_heads(y, logits, heads: int, tokens: int, head_dim: int, stream=None) -> None:
+    check(load().ltx25_gate_heads(_stream(stream), _ptr(y), _ptr(logits), heads, tokens,
+                                  head_dim))
 
 
 def dequant(w: QWeight, out, N: int, K: int, stream=None) -> None:

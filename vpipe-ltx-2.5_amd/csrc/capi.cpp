@@ -467,6 +467,22 @@ int ltx25_gelu_tanh(void* stream, const void* x, void* y, size_t n)
   return e == hipSuccess ? LTX25_OK : hip_fail(e, "gelu launch");
 }
 
+int ltx25_gate_heads(void* stream, void* y, const void* logits, int heads, int tokens,
+                     int head_dim)
+{
+  if (heads <= 0 || tokens <= 0 || head_dim <= 0) { return LTX25_OK; }
+  if (y == nullptr || logits == nullptr) { return fail(LTX25_E_INVAL, "y or logits is null"); }
+  if ((((uintptr_t)y | (uintptr_t)logits) & 1u) != 0) {
+    return fail(LTX25_E_INVAL, "a bf16 tensor is not 2-byte aligned");
+  }
+  DeviceState* ds = nullptr;
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_gate_heads((uint16_t*)y, (const uint16_t*)logits, heads,
+                                                tokens, head_dim, (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "gate_heads launch");
+}
+
 int ltx25_dequant(void* stream, const ltx25_qweight* w, void* out_bf16, int N,
                   int K)
 {

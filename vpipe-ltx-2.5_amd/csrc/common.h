@@ -140,6 +140,9 @@ hipError_t launch_bias_add(uint16_t* y, const void* bias, int bias_type,
                            int M, int N, hipStream_t stream);
 hipError_t launch_gelu(const uint16_t* x, uint16_t* y, size_t n,
                        hipStream_t stream);
+// y [tokens][heads][head_dim] bf16 *= 2 sigmoid(logits [tokens][heads] bf16), in place.
+hipError_t launch_gate_heads(uint16_t* y, const uint16_t* logits, int heads, int tokens,
+                             int head_dim, hipStream_t stream);
 hipError_t launch_dequant(const void* codes, const uint16_t* scales,
                           const uint16_t* qbias, int bits, int group,
                           uint16_t* out, int N, int K, hipStream_t stream);

@@ -65,6 +65,37 @@ gelu_kernel(const uint16_t* x, uint16_t* y, size_t n)
   }
 }
 
+// Per-head gate on the attention output, y[t][h][d] *= 2 sigmoid(logit[t][h]),
+// rounded once to bf16 (the reference rounds y to its storage type there
+// too). Eight d per thread: one 16-byte load and store when the head width
+// allows it, else element by element.
+__global__ void __launch_bounds__(kBlock)
+gate_heads_kernel(uint16_t* y, const uint16_t* logits, int heads, int head_dim,
+                  size_t chunks_per_row, size_t total_chunks, bool vec)
+{
+  const size_t c = (size_t)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= total_chunks) { return; }
+  const size_t row = c / chunks_per_row;          // token t * heads + h
+  const int d0 = (int)(c % chunks_per_row) * 8;
+  const float lg = bf16_to_f32(logits[row]);
+  const float g = 2.0f / (1.0f + expf(-lg));
+  uint16_t* p = y + row * (size_t)head_dim + d0;
+  if (vec) {
+    const uint4 v = *(const uint4*)p;
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      w[j] = pack_bf16x2(bf16_to_f32((uint16_t)(w[j] & 0xffffu)) * g,
+                         bf16_to_f32((uint16_t)(w[j] >> 16)) * g);
+    }
+    *(uint4*)p = make_uint4(w[0], w[1], w[2], w[3]);
+    return;
+  }
+  for (int d = d0; d < d0 + 8 && d < head_dim; ++d) {
+    p[d - d0] = f32_to_bf16(bf16_to_f32(p[d - d0]) * g);
+  }
+}
+
 // Dequant-once: 16 codes (w8) or 32 codes (w4) per thread, one 16-byte
 // load, w = bf16(fma(scale, q, qbias)) stored as 2 or 4 16-byte stores.
 template <int BITS>
@@ -227,6 +258,18 @@ hipError_t launch_gelu(const uint16_t* x, uint16_t* y, size_t n,
 {
   hipLaunchKernelGGL(gelu_kernel, dim3(blocks_for((n + 7) / 8)), dim3(kBlock),
                      0, stream, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_gate_heads(uint16_t* y, const uint16_t* logits, int heads, int tokens,
+                             int head_dim, hipStream_t stream)
+{
+  const size_t chunks_per_row = ((size_t)head_dim + 7) / 8;
+  const size_t total = (size_t)tokens * heads * chunks_per_row;
+  if (total == 0) { return hipSuccess; }
+  const bool vec = head_dim % 8 == 0 && ((uintptr_t)y & 15u) == 0;
+  hipLaunchKernelGGL(gate_heads_kernel, dim3(blocks_for(total)), dim3(kBlock), 0, stream, y,
+                     logits, heads, head_dim, chunks_per_row, total, vec);
   return hipGetLastError();
 }
 

@@ -95,6 +95,13 @@ public:
     note(ltx25_gelu_tanh(enc, x, y, (size_t)n));
   }
 
+  // y[t][h][d] *= 2 sigmoid(logits[t][h]) (src/ltx25-metal-ops.cc:1089-1101).
+  void gate_heads(hipStream_t enc, void* y, const void* logits, int heads, int tokens,
+                  int head_dim) const
+  {
+    note(ltx25_gate_heads(enc, y, logits, heads, tokens, head_dim));
+  }
+
   // y[M][N] += (x . a^T) . b^T (src/ltx25-metal-ops.h:107-133). `r` and `d`
   // keep the reference signature's caller scratch; the fused kernel uses
   // neither.
