@@ -592,7 +592,9 @@ qgemm_kernel(KParams p)
       const uint4 v = *(const uint4*)(srow + c);
       uint16_t* dst = p.y + (size_t)m * p.N + n;
       if (vec_rows && n + 8 <= p.N) {
-        *(uint4*)dst = v;
+        // non-temporal: the tile is not read again by this launch (measured
+        // +0.5% on the FFN GEMMs, whose stores leave in one chip-wide burst)
+        __builtin_nontemporal_store(__builtin_bit_cast(i32x4, v), (i32x4*)dst);
       } else {
         const uint16_t e[8] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y,
                                (uint16_t)(v.y >> 16), (uint16_t)v.z, (uint16_t)(v.z >> 16),
