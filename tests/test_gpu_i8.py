@@ -38,10 +38,10 @@ def quantize_rows_dev(pkg, x_dev, M, K):
     return q, s
 
 
-def test_quantize_rows_bit_exact(pkg):
-    say("i8 quantize rows")
-    M, K = 70, 4096
-    rng = np.random.default_rng(30)
+@pytest.mark.parametrize("M,K", [(70, 4096), (9, 20480)])   # 20480: past the register cache
+def test_quantize_rows_bit_exact(pkg, M, K):
+    say(f"i8 quantize rows M={M} K={K}")
+    rng = np.random.default_rng(30 + K)
     x = orc.bf16_rne(rng_normal(rng, (M, K)))
     x[4] = 0
     x[5, 17] = orc.bf16_rne(np.array([300.0], np.float32))[0]   # one outlier
@@ -51,11 +51,15 @@ def test_quantize_rows_bit_exact(pkg):
     assert np.array_equal(q.cpu().numpy(), q_ref)
 
 
-def test_quantize_qweight_bit_exact(pkg):
-    say("i8 quantize of a w8g64 weight")
-    N, K = 48, 2048
-    rng = np.random.default_rng(31)
-    qw, codes, scales, biases, wb = make_qweight(pkg, rng_normal(rng, (N, K), 0.02), 8, 64)
+@pytest.mark.parametrize("N,K,bits,group", [
+    (48, 2048, 8, 64), (40, 4096, 8, 32), (33, 4096, 4, 64), (17, 2048, 4, 32),
+    (6, 36864, 8, 64),     # w8: 2304 chunks per row, past the register cache
+    (4, 69632, 4, 64),     # w4: 2176 chunks per row
+])
+def test_quantize_qweight_bit_exact(pkg, N, K, bits, group):
+    say(f"i8 quantize of a w{bits}g{group} weight N={N} K={K}")
+    rng = np.random.default_rng(31 + K + bits)
+    qw, codes, scales, biases, wb = make_qweight(pkg, rng_normal(rng, (N, K), 0.02), bits, group)
     wq = torch.empty((N, K), dtype=torch.int8, device="cuda")
     sw = torch.empty((N,), dtype=torch.float32, device="cuda")
     pkg.i8_quantize_qweight(qw, wq, sw, N, K)

@@ -622,6 +622,10 @@ int ltx25_i8_quantize_qweight(void* stream, const ltx25_qweight* w,
   if (rc != LTX25_OK) { return rc; }
   hipError_t e;
   if (w->quantized) {
+    // 16-byte code loads and int8 stores
+    if (check_aligned("codes", w->codes) != LTX25_OK || check_aligned("wq", wq) != LTX25_OK) {
+      return LTX25_E_INVAL;
+    }
     e = ltx25::launch_i8_quantize_qweight(w->codes, (const uint16_t*)w->scales,
                                           (const uint16_t*)w->qbias, w->bits, w->group,
                                           wq, sw, N, K, (hipStream_t)stream);

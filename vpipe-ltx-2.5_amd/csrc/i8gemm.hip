@@ -16,8 +16,33 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// One workgroup per row: absmax, then q = clamp(rint(x / s), -127, 127).
-// Works on bf16 activations (values exact in f32).
+// Rows longer than kCacheChunks 16-byte chunks per thread are re-read for
+// the second pass; up to that they stay in registers between the passes.
+constexpr int kCacheChunks = 8;
+
+__device__ __forceinline__ uint32_t q8(float v, float s)
+{
+  float r = 0.0f;
+  if (s > 0.0f) {
+    r = rintf(v / s);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+  }
+  return (uint32_t)(int)r & 0xffu;
+}
+
+__device__ __forceinline__ float block_absmax(float amax, float* red)
+{
+  for (int off = 32; off > 0; off >>= 1) {
+    amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  }
+  if ((threadIdx.x & 63) == 0) { red[threadIdx.x >> 6] = amax; }
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// One workgroup per row: absmax, then q = clamp(rint(x / s), -127, 127),
+// s = absmax / 127. Works on bf16 activations (values exact in f32); the
+// row is read once, 16 bytes (8 values) per load.
 __global__ void __launch_bounds__(kThreads)
 i8_quantize_rows_kernel(const uint16_t* x, int8_t* q, float* scale, int K)
 {
@@ -25,45 +50,55 @@ i8_quantize_rows_kernel(const uint16_t* x, int8_t* q, float* scale, int K)
   const int m = blockIdx.x;
   const uint16_t* xr = x + (size_t)m * K;
   int8_t* qr = q + (size_t)m * K;
+  const int chunks = K / 8;
+  uint4 cache[kCacheChunks];
   float amax = 0.0f;
-  for (int k = threadIdx.x * 8; k < K; k += kThreads * 8) {
-    const uint4 v = *(const uint4*)(xr + k);
+  auto absmax8 = [&](const uint4& v) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       amax = fmaxf(amax, fabsf(bf16_to_f32((uint16_t)(w[j] & 0xffffu))));
       amax = fmaxf(amax, fabsf(bf16_to_f32((uint16_t)(w[j] >> 16))));
     }
+  };
+#pragma unroll
+  for (int c = 0; c < kCacheChunks; ++c) {
+    const int i = (int)threadIdx.x + c * kThreads;
+    if (i < chunks) {
+      cache[c] = *(const uint4*)(xr + (size_t)i * 8);
+      absmax8(cache[c]);
+    }
   }
-  for (int off = 32; off > 0; off >>= 1) {
-    amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  for (int i = (int)threadIdx.x + kCacheChunks * kThreads; i < chunks; i += kThreads) {
+    absmax8(*(const uint4*)(xr + (size_t)i * 8));
   }
-  if ((threadIdx.x & 63) == 0) { red[threadIdx.x >> 6] = amax; }
-  __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  amax = block_absmax(amax, red);
   const float s = amax / 127.0f;
   if (threadIdx.x == 0) { scale[m] = s; }
-  for (int k = threadIdx.x * 8; k < K; k += kThreads * 8) {
-    const uint4 v = *(const uint4*)(xr + k);
+  auto quant8 = [&](const uint4& v, int i) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     uint32_t packed[2] = {0u, 0u};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint16_t h = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
-      float r = 0.0f;
-      if (s > 0.0f) {
-        r = rintf(bf16_to_f32(h) / s);
-        r = fminf(fmaxf(r, -127.0f), 127.0f);
-      }
-      packed[j >> 2] |= ((uint32_t)(int)r & 0xffu) << (8 * (j & 3));
+      packed[j >> 2] |= q8(bf16_to_f32(h), s) << (8 * (j & 3));
     }
-    *(uint2*)(qr + k) = make_uint2(packed[0], packed[1]);
+    *(uint2*)(qr + (size_t)i * 8) = make_uint2(packed[0], packed[1]);
+  };
+#pragma unroll
+  for (int c = 0; c < kCacheChunks; ++c) {
+    const int i = (int)threadIdx.x + c * kThreads;
+    if (i < chunks) { quant8(cache[c], i); }
+  }
+  for (int i = (int)threadIdx.x + kCacheChunks * kThreads; i < chunks; i += kThreads) {
+    quant8(*(const uint4*)(xr + (size_t)i * 8), i);
   }
 }
 
-// The same for the dequantized values of a group-affine weight row:
-// w = bf16(fma(scale, q, qbias)), read from the codes twice (absmax pass,
-// then the quantize pass) rather than materialised.
+// The same for the dequantized values of a group-affine weight row,
+// w = bf16(fma(scale, q, qbias)): one 16-byte load of codes (16 w8 or 32 w4
+// codes, all in one group) per chunk, kept in registers between the absmax
+// and the quantize pass; 16-byte int8 stores.
 template <int BITS>
 __global__ void __launch_bounds__(kThreads)
 i8_quantize_qweight_kernel(const uint8_t* codes, const uint16_t* scales,
@@ -71,40 +106,74 @@ i8_quantize_qweight_kernel(const uint8_t* codes, const uint16_t* scales,
                            int8_t* q, float* scale, int K)
 {
   __shared__ float red[kThreads / 64];
+  constexpr int CPC = 128 / BITS;                 // codes per 16-byte chunk
   const int n = blockIdx.x;
-  const size_t row_bytes = (size_t)K * BITS / 8;
-  const uint8_t* cr = codes + (size_t)n * row_bytes;
-  auto value = [&](int k) -> float {
-    uint32_t c;
-    if constexpr (BITS == 8) {
-      c = cr[k];
-    } else {
-      c = (cr[k >> 1] >> (4 * (k & 1))) & 0xfu;
-    }
-    const size_t gi = (size_t)n * gcols + (k >> gshift);
-    const float d = fmaf(bf16_to_f32(scales[gi]), (float)c, bf16_to_f32(qbias[gi]));
-    return bf16_to_f32(f32_to_bf16(d));
-  };
+  const uint8_t* cr = codes + (size_t)n * ((size_t)K * BITS / 8);
+  const uint16_t* srow = scales + (size_t)n * gcols;
+  const uint16_t* brow = qbias + (size_t)n * gcols;
+  int8_t* qr = q + (size_t)n * K;
+  const int chunks = K / CPC;
+  uint4 cache[kCacheChunks];
   float amax = 0.0f;
-  for (int k = threadIdx.x; k < K; k += kThreads) {
-    amax = fmaxf(amax, fabsf(value(k)));
+  // the CPC dequantized values of chunk i, in order, into v
+  auto dequant = [&](const uint4& c, int i, float* v) {
+    const int g = (i * CPC) >> gshift;
+    const float s = bf16_to_f32(srow[g]);
+    const float b = bf16_to_f32(brow[g]);
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int j = 0; j < CPC; ++j) {
+      uint32_t code;
+      if constexpr (BITS == 8) {
+        code = (w[j >> 2] >> (8 * (j & 3))) & 0xffu;
+      } else {
+        code = (w[j >> 3] >> (4 * (j & 7))) & 0xfu;
+      }
+      v[j] = bf16_to_f32(f32_to_bf16(fmaf(s, (float)code, b)));
+    }
+  };
+  auto absmax_chunk = [&](const uint4& c, int i) {
+    float v[CPC];
+    dequant(c, i, v);
+#pragma unroll
+    for (int j = 0; j < CPC; ++j) { amax = fmaxf(amax, fabsf(v[j])); }
+  };
+#pragma unroll
+  for (int c = 0; c < kCacheChunks; ++c) {
+    const int i = (int)threadIdx.x + c * kThreads;
+    if (i < chunks) {
+      cache[c] = *(const uint4*)(cr + (size_t)i * 16);
+      absmax_chunk(cache[c], i);
+    }
   }
-  for (int off = 32; off > 0; off >>= 1) {
-    amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  for (int i = (int)threadIdx.x + kCacheChunks * kThreads; i < chunks; i += kThreads) {
+    absmax_chunk(*(const uint4*)(cr + (size_t)i * 16), i);
   }
-  if ((threadIdx.x & 63) == 0) { red[threadIdx.x >> 6] = amax; }
-  __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  amax = block_absmax(amax, red);
   const float s = amax / 127.0f;
   if (threadIdx.x == 0) { scale[n] = s; }
-  int8_t* qr = q + (size_t)n * K;
-  for (int k = threadIdx.x; k < K; k += kThreads) {
-    float r = 0.0f;
-    if (s > 0.0f) {
-      r = rintf(value(k) / s);
-      r = fminf(fmaxf(r, -127.0f), 127.0f);
+  auto quant_chunk = [&](const uint4& c, int i) {
+    float v[CPC];
+    dequant(c, i, v);
+    uint32_t packed[CPC / 4];
+#pragma unroll
+    for (int t = 0; t < CPC / 4; ++t) {
+      packed[t] = q8(v[4 * t], s) | (q8(v[4 * t + 1], s) << 8) | (q8(v[4 * t + 2], s) << 16) |
+                  (q8(v[4 * t + 3], s) << 24);
     }
-    qr[k] = (int8_t)(int)r;
+#pragma unroll
+    for (int t = 0; t < CPC / 16; ++t) {
+      *(uint4*)(qr + (size_t)i * CPC + 16 * t) =
+          make_uint4(packed[4 * t], packed[4 * t + 1], packed[4 * t + 2], packed[4 * t + 3]);
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < kCacheChunks; ++c) {
+    const int i = (int)threadIdx.x + c * kThreads;
+    if (i < chunks) { quant_chunk(cache[c], i); }
+  }
+  for (int i = (int)threadIdx.x + kCacheChunks * kThreads; i < chunks; i += kThreads) {
+    quant_chunk(*(const uint4*)(cr + (size_t)i * 16), i);
   }
 }
 
