@@ -151,6 +151,10 @@ qgemm_kernel(KParams p)
 
   __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BM * kLdsRow];
   __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][BN * kLdsRow];
+  // The epilogue's per-column bias (as f32) and, for the int8 GEMM, per-column
+  // and per-row scales, staged during the prologue so that the epilogue does
+  // not wait on global loads.
+  __shared__ float lds_ep[2 * BN + BM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -469,8 +473,35 @@ qgemm_kernel(KParams p)
     // Two LDS stages; the last two steps are peeled so that the
     // steady-state body has no branches.
     load_regs(kbeg);
+    // the epilogue's operands, fetched under the first operand loads
+    float ep_v[(2 * BN + BM + NT - 1) / NT];
+    if constexpr (!SPLIT) {
+#pragma unroll
+      for (int u = 0; u < (2 * BN + BM + NT - 1) / NT; ++u) {
+        const int e = tid + u * NT;
+        float v = 0.0f;
+        if (e < BN) {
+          const int n = n0 + e;
+          v = n < p.N ? load_bias(p.bias, p.bias_type, n) : 0.0f;
+        } else if (e < 2 * BN) {
+          const int n = n0 + e - BN;
+          v = I8 && n < p.N ? p.sw[n] : 0.0f;
+        } else if (e < 2 * BN + BM) {
+          const int m = m0 + e - 2 * BN;
+          v = I8 && m < p.M ? p.sx[m] : 0.0f;
+        }
+        ep_v[u] = v;
+      }
+    }
     store_a(0);
     store_b(0);
+    if constexpr (!SPLIT) {
+#pragma unroll
+      for (int u = 0; u < (2 * BN + BM + NT - 1) / NT; ++u) {
+        const int e = tid + u * NT;
+        if (e < 2 * BN + BM) { lds_ep[e] = ep_v[u]; }
+      }
+    }
     if (nsteps > 1) { load_regs(kbeg + SK); }
     __syncthreads();
     read_frags(0, 0, 0);
@@ -535,8 +566,9 @@ qgemm_kernel(KParams p)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int n = n0 + wn * WTN + j * 32 + g * 8 + lcol + t;
-          bv[g][t] = n < p.N ? load_bias(p.bias, p.bias_type, n) : 0.0f;
-          swv[g][t] = I8 && n < p.N ? p.sw[n] : 0.0f;
+          const int c = wn * WTN + j * 32 + g * 8 + lcol + t;
+          bv[g][t] = n < p.N ? lds_ep[c] : 0.0f;
+          swv[g][t] = I8 && n < p.N ? lds_ep[BN + c] : 0.0f;
         }
       }
 #pragma unroll
@@ -544,7 +576,7 @@ qgemm_kernel(KParams p)
         const int r = wm * WTM + i * 32 + lrow;
         uint16_t* srow = r < BM / 2 ? stage_lo + r * EP : stage_hi + (r - BM / 2) * EP;
         const int m = m0 + r;
-        const float sxm = I8 && m < p.M ? p.sx[m] : 0.0f;
+        const float sxm = I8 && m < p.M ? lds_ep[2 * BN + r] : 0.0f;
         if constexpr (I8) {
           // the raw int32 accumulators, when asked for (bit-exact checks)
           if (p.acc_out != nullptr && m < p.M) {
