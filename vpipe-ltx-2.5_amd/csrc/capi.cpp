@@ -12,6 +12,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -22,15 +23,21 @@ namespace {
 
 thread_local std::string g_err;
 
-int fail(int code, const char* fmt, ...)
+int vfail(int code, const char* fmt, va_list ap)
 {
   char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
   std::vsnprintf(buf, sizeof buf, fmt, ap);
-  va_end(ap);
   g_err = buf;
   return code;
+}
+
+int fail(int code, const char* fmt, ...)
+{
+  va_list ap;
+  va_start(ap, fmt);
+  const int rc = vfail(code, fmt, ap);
+  va_end(ap);
+  return rc;
 }
 
 }  // namespace
@@ -39,13 +46,11 @@ namespace ltx25 {
 
 int set_error(int code, const char* fmt, ...)
 {
-  char buf[512];
   va_list ap;
   va_start(ap, fmt);
-  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  const int rc = vfail(code, fmt, ap);
   va_end(ap);
-  g_err = buf;
-  return code;
+  return rc;
 }
 
 }  // namespace ltx25
@@ -79,8 +84,10 @@ struct DeviceState {
 
 std::mutex g_mu;
 DeviceState g_dev[kMaxDevices];
-int g_i8_on = 0;
-int g_deq_once = LTX25_DEQUANT_ONCE_AUTO;
+// Process-wide switches (the reference keeps them per MetalOps; one set per
+// process here), read on every call from any thread.
+std::atomic<int> g_i8_on{0};
+std::atomic<int> g_deq_once{LTX25_DEQUANT_ONCE_AUTO};
 
 // Check (once per device) that the current device is gfx950.
 int current_device(DeviceState** out)
@@ -511,15 +518,16 @@ int ltx25_set_dequant_once(int mode)
       mode != LTX25_DEQUANT_ONCE_AUTO) {
     return fail(LTX25_E_INVAL, "dequant-once mode %d is not OFF, ON or AUTO", mode);
   }
-  g_deq_once = mode;
+  g_deq_once.store(mode, std::memory_order_relaxed);
   return LTX25_OK;
 }
 
 int ltx25_dequant_once_takes(int M, int K, int N)
 {
-  if (g_deq_once == LTX25_DEQUANT_ONCE_OFF) { return 0; }
+  const int mode = g_deq_once.load(std::memory_order_relaxed);
+  if (mode == LTX25_DEQUANT_ONCE_OFF) { return 0; }
   if (M < 64 || N < 16 || K <= 0 || K % 64 != 0) { return 0; }
-  return g_deq_once == LTX25_DEQUANT_ONCE_ON || M >= LTX25_DEQUANT_ONCE_AUTO_MIN_M ? 1 : 0;
+  return mode == LTX25_DEQUANT_ONCE_ON || M >= LTX25_DEQUANT_ONCE_AUTO_MIN_M ? 1 : 0;
 }
 
 int ltx25_lora_on_matrix_cores(int M, int K, int N, int rank)
@@ -582,13 +590,16 @@ int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
 
 int ltx25_set_i8_gemm(int on)
 {
-  g_i8_on = on != 0;
+  g_i8_on.store(on != 0 ? 1 : 0, std::memory_order_relaxed);
   return LTX25_OK;
 }
 
 int ltx25_i8_takes(int M, int K, int N)
 {
-  return g_i8_on && M >= 1024 && K >= 1024 && K % 128 == 0 && N >= 16 ? 1 : 0;
+  return g_i8_on.load(std::memory_order_relaxed) != 0 && M >= 1024 && K >= 1024 &&
+                 K % 128 == 0 && N >= 16
+             ? 1
+             : 0;
 }
 
 int ltx25_i8_quantize_rows(void* stream, const void* x_bf16, int8_t* q,
