@@ -259,7 +259,7 @@ int run_linear(hipStream_t st, const void* x, const ltx25_qweight* w,
   d.M = M;
   d.N = N;
   d.K = K;
-  const ltx25::GemmPlan plan = ltx25::plan_gemm(M, N, K, ds->cu_count);
+  const ltx25::GemmPlan plan = ltx25::plan_gemm(M, N, K, d.bits, ds->cu_count);
   float* ws = nullptr;
   if (plan.workspace_bytes > 0) {
     std::lock_guard<std::mutex> lk(g_mu);
@@ -382,7 +382,7 @@ int lora_pair(DeviceState* ds, hipStream_t st, const void* x, const void* a, con
       d.N = N;
       d.K = rk;
     }
-    const ltx25::GemmPlan plan = ltx25::plan_gemm(d.M, d.N, d.K, ds->cu_count);
+    const ltx25::GemmPlan plan = ltx25::plan_gemm(d.M, d.N, d.K, d.bits, ds->cu_count);
     float* ws = nullptr;
     if (plan.workspace_bytes > 0) {
       std::lock_guard<std::mutex> lk(g_mu);

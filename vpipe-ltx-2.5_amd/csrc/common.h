@@ -109,15 +109,27 @@ struct GemmDesc {
 
 // The tile configuration a GEMM runs with, chosen on the host.
 struct GemmPlan {
-  int tile = 0;      // 0 = 256x256 (tall), 1 = 128x128 (skinny / mid)
+  int tile = 0;      // 0 = 256x256 (tall), 1 = 128x128 (mid), 2 = M <= 128 (skinny.hip)
   int splits = 1;    // split-K factor
   int k_chunk = 0;   // K elements per split (multiple of 64)
   size_t workspace_bytes = 0;   // f32 partials when splits > 1
 };
 
-GemmPlan plan_gemm(int M, int N, int K, int cu_count);
+// `bits` is the weight format the GEMM reads: 8 or 4 (codes) or 16 (dense).
+GemmPlan plan_gemm(int M, int N, int K, int bits, int cu_count);
 hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
                        float* workspace, hipStream_t stream);
+// The M <= 128 route (skinny.hip): 32 output columns per workgroup, K split
+// between its 8 waves, and across workgroups above 2048. Fills `plan` and
+// returns true when it takes the shape.
+bool plan_skinny(int M, int N, int K, int bits, GemmPlan& plan);
+hipError_t launch_skinny(const GemmDesc& d, const GemmPlan& plan, float* workspace,
+                         hipStream_t stream);
+// Sums `splits` f32 partial planes [M][N] in split order, adds bias and
+// y_in, applies the epilogue and rounds to bf16 once.
+hipError_t launch_splitk_reduce(const float* partial, int splits, const void* bias, int bias_type,
+                                int epilogue, const uint16_t* y_in, uint16_t* y, int M, int N,
+                                hipStream_t stream);
 
 // The low-rank adapter delta y += (x . A^T) . B^T (lora.hip). One launch
 // covers at most kLoraMaxRank adapter columns: `a` points at the pass's

@@ -731,9 +731,10 @@ int ilog2(int v)
 
 }  // namespace
 
-GemmPlan plan_gemm(int M, int N, int K, int cu_count)
+GemmPlan plan_gemm(int M, int N, int K, int bits, int cu_count)
 {
   GemmPlan plan;
+  if (plan_skinny(M, N, K, bits, plan)) { return plan; }
   const long tall_tiles = (long)((M + 255) / 256) * ((N + 255) / 256);
   if (M > 128 && tall_tiles >= cu_count) {
     plan.tile = 0;
@@ -792,9 +793,21 @@ hipError_t launch_i8_gemm(const int8_t* xq, const float* sx, const int8_t* wq, c
   return launch_cfg<128, 128, 2, 2, kI8Ops, false>(kp, 1, stream);
 }
 
+hipError_t launch_splitk_reduce(const float* partial, int splits, const void* bias, int bias_type,
+                                int epilogue, const uint16_t* y_in, uint16_t* y, int M, int N,
+                                hipStream_t stream)
+{
+  const size_t total = (size_t)M * N;
+  const unsigned blocks = (unsigned)((total + 1023) / 1024);
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, splits,
+                     bias, bias != nullptr ? bias_type : kBiasNone, epilogue, y_in, y, M, N);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
                        float* workspace, hipStream_t stream)
 {
+  if (plan.tile == 2) { return launch_skinny(d, plan, workspace, stream); }
   KParams kp = {};
   kp.x = d.x;
   kp.wq = (const uint8_t*)d.w;
@@ -823,12 +836,8 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
                      : launch_tile<128, kSkinnyBN, 2 * 128 / kSkinnyBN, kSkinnyBN / 64>(
                            kp, d.bits, plan.splits, stream);
   if (e != hipSuccess || plan.splits <= 1) { return e; }
-  const size_t total = (size_t)d.M * d.N;
-  const unsigned blocks = (unsigned)((total + 1023) / 1024);
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream,
-                     (const float*)workspace, plan.splits, kp.bias,
-                     kp.bias_type, d.epilogue, d.y_in, d.y, d.M, d.N);
-  return hipGetLastError();
+  return launch_splitk_reduce(workspace, plan.splits, kp.bias, kp.bias_type, d.epilogue, d.y_in,
+                              d.y, d.M, d.N, stream);
 }
 
 }  // namespace ltx25
