@@ -96,52 +96,70 @@ gate_heads_kernel(uint16_t* y, const uint16_t* logits, int heads, int head_dim,
   }
 }
 
-// Dequant-once: 16 codes (w8) or 32 codes (w4) per thread, one 16-byte
-// load, w = bf16(fma(scale, q, qbias)) stored as 2 or 4 16-byte stores.
+// Dequant-once: one thread per run of 8 codes (8 bytes of w8, 4 of w4) ->
+// 8 bf16 (16 bytes), w = bf16(fma(scale, q, qbias)). Block (row n, part p)
+// covers kBlock * kDeqRuns consecutive runs of row n and consecutive lanes
+// take consecutive runs, so each load and each store instruction is one
+// contiguous span of the row; each thread has kDeqRuns runs in flight.
+constexpr int kDeqRuns = 2;
+
 template <int BITS>
 __global__ void __launch_bounds__(kBlock)
 dequant_kernel(const uint8_t* codes, const uint16_t* scales,
                const uint16_t* qbias, int gshift, int gcols, uint16_t* out,
                int N, int K)
 {
-  constexpr int CPC = 128 / BITS;          // codes per 16-byte chunk
-  const int chunks_per_row = K / CPC;
-  const size_t c = (size_t)blockIdx.x * kBlock + threadIdx.x;
-  if (c >= (size_t)N * chunks_per_row) { return; }
-  const int n = (int)(c / chunks_per_row);
-  const int k0 = (int)(c % chunks_per_row) * CPC;
-  const uint4 v = *(const uint4*)(codes + (size_t)n * K * BITS / 8 + (size_t)k0 * BITS / 8);
-  const size_t gi = (size_t)n * gcols + (k0 >> gshift);
-  const float s = bf16_to_f32(scales[gi]);
-  const float b = bf16_to_f32(qbias[gi]);
-  const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-  uint16_t* dst = out + (size_t)n * K + k0;
-  if constexpr (BITS == 8) {
-    uint32_t o[8];
+  const int n = blockIdx.x;
+  const int runs = K >> 3;
+  const int r0 = blockIdx.y * kBlock * kDeqRuns + threadIdx.x;
+  const uint8_t* crow = codes + (size_t)n * K * BITS / 8;
+  const uint16_t* srow = scales + (size_t)n * gcols;
+  const uint16_t* qrow = qbias + (size_t)n * gcols;
+  uint16_t* orow = out + (size_t)n * K;
+  uint32_t v[kDeqRuns][2];
+  float s[kDeqRuns], b[kDeqRuns];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o[2 * j] = pack_bf16x2(fmaf(s, (float)(wv[j] & 0xffu), b),
-                             fmaf(s, (float)((wv[j] >> 8) & 0xffu), b));
-      o[2 * j + 1] = pack_bf16x2(fmaf(s, (float)((wv[j] >> 16) & 0xffu), b),
-                                 fmaf(s, (float)(wv[j] >> 24), b));
+  for (int j = 0; j < kDeqRuns; ++j) {
+    const int r = r0 + j * kBlock;
+    v[j][0] = v[j][1] = 0u;
+    s[j] = b[j] = 0.0f;
+    if (r < runs) {
+      if constexpr (BITS == 8) {
+        const uint2 c = *(const uint2*)(crow + (size_t)r * 8);
+        v[j][0] = c.x;
+        v[j][1] = c.y;
+      } else {
+        v[j][0] = *(const uint32_t*)(crow + (size_t)r * 4);
+      }
+      const int g = (r << 3) >> gshift;
+      s[j] = bf16_to_f32(srow[g]);
+      b[j] = bf16_to_f32(qrow[g]);
     }
-    *(uint4*)dst = make_uint4(o[0], o[1], o[2], o[3]);
-    *(uint4*)(dst + 8) = make_uint4(o[4], o[5], o[6], o[7]);
-  } else {
-    uint32_t o[16];
+  }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < kDeqRuns; ++j) {
+    const int r = r0 + j * kBlock;
+    if (r >= runs) { return; }
+    uint32_t o[4];
+    if constexpr (BITS == 8) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t w = v[j][h];
+        o[2 * h] = pack_bf16x2(fmaf(s[j], (float)(w & 0xffu), b[j]),
+                               fmaf(s[j], (float)((w >> 8) & 0xffu), b[j]));
+        o[2 * h + 1] = pack_bf16x2(fmaf(s[j], (float)((w >> 16) & 0xffu), b[j]),
+                                   fmaf(s[j], (float)(w >> 24), b[j]));
+      }
+    } else {
+      // code c at bits 4c of the word
+      const uint32_t w = v[j][0];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const uint32_t q0 = (wv[j] >> (8 * t)) & 0xfu;
-        const uint32_t q1 = (wv[j] >> (8 * t + 4)) & 0xfu;
-        o[4 * j + t] = pack_bf16x2(fmaf(s, (float)q0, b), fmaf(s, (float)q1, b));
+        o[t] = pack_bf16x2(fmaf(s[j], (float)((w >> (8 * t)) & 0xfu), b[j]),
+                           fmaf(s[j], (float)((w >> (8 * t + 4)) & 0xfu), b[j]));
       }
     }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      *(uint4*)(dst + 8 * t) = make_uint4(o[4 * t], o[4 * t + 1], o[4 * t + 2], o[4 * t + 3]);
-    }
+    *(uint4*)(orow + (size_t)r * 8) = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
 
@@ -277,18 +295,16 @@ hipError_t launch_dequant(const void* codes, const uint16_t* scales,
                           const uint16_t* qbias, int bits, int group,
                           uint16_t* out, int N, int K, hipStream_t stream)
 {
-  const int cpc = 128 / bits;
-  const size_t chunks = (size_t)N * (K / cpc);
   const int gshift = ilog2(group);
   const int gcols = K / group;
+  const int parts = (K / 8 + kBlock * kDeqRuns - 1) / (kBlock * kDeqRuns);
+  const dim3 grid((unsigned)N, (unsigned)parts, 1);
   if (bits == 8) {
-    hipLaunchKernelGGL(dequant_kernel<8>, dim3(blocks_for(chunks)),
-                       dim3(kBlock), 0, stream, (const uint8_t*)codes, scales,
-                       qbias, gshift, gcols, out, N, K);
+    hipLaunchKernelGGL(dequant_kernel<8>, grid, dim3(kBlock), 0, stream,
+                       (const uint8_t*)codes, scales, qbias, gshift, gcols, out, N, K);
   } else {
-    hipLaunchKernelGGL(dequant_kernel<4>, dim3(blocks_for(chunks)),
-                       dim3(kBlock), 0, stream, (const uint8_t*)codes, scales,
-                       qbias, gshift, gcols, out, N, K);
+    hipLaunchKernelGGL(dequant_kernel<4>, grid, dim3(kBlock), 0, stream,
+                       (const uint8_t*)codes, scales, qbias, gshift, gcols, out, N, K);
   }
   return hipGetLastError();
 }
