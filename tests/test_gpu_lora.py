@@ -7,7 +7,9 @@ distilled adapter's rank 450), with its bar -- rel-L2 < 2e-2 against f64 over
 the unrounded draws -- and the north-star bar against the oracle, which
 applies the same bf16 rounding of r: max|y - ref| / max|ref| <= 1e-2. Plus the
 shapes that take the element-wise load path, an adapter wider than one launch
-(rank > 512), the empty-shape no-op and A = 0 (y bit-identical).
+(rank > 512), the matrix-core GEMM pair (rank >= 96), the r-first route (many
+tokens: r by the dense GEMM, then the fused kernel's second phase), the
+empty-shape no-op and A = 0 (y bit-identical).
 """
 import zlib
 
@@ -44,6 +46,11 @@ SHAPES = [
     ("GEMM pair, rank 450 padded to 512", 512, 1024, 2048, 450),
     ("GEMM pair, ragged M and N", 777, 512, 1000, 200),
     ("GEMM pair, rank 1000 (split-K second GEMM)", 256, 512, 640, 1000),
+    # r first (M >= 512, rank % 8 == 0, rank < 96): r = x . A^T by the dense GEMM, then the
+    # fused kernel's second phase reads it
+    ("r first: rank 32 at the FFN width", 1024, 4096, 16384, 32),
+    ("r first: rank 40, ragged M", 777, 1024, 2048, 40),
+    ("r first: rank 8", 600, 512, 1024, 8),
 ]
 
 

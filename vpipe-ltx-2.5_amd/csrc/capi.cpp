@@ -321,6 +321,9 @@ int run_i8_linear(DeviceState* ds, hipStream_t st, const void* x,
 // kLoraPairMinRank up, where the adapter's FLOPs outweigh re-reading y:
 // below it the fused one-pass kernel, bound by y's traffic, is faster.
 constexpr int kLoraPairMinRank = 96;
+// From this many tokens a narrow adapter's r = x . A^T is computed once by
+// the dense GEMM rather than per column split inside the fused kernel.
+constexpr int kLoraRFirstMinM = 512;
 
 bool lora_pair_takes(int M, int K, int N, int rank, const void* x, const void* y)
 {
@@ -577,6 +580,43 @@ int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
     if (e != hipSuccess) { return hip_fail(e, "lora pad launch"); }
     pb = (const uint16_t*)ds->lora_b;
     ldb = rank8;
+  }
+  if (vec && M >= kLoraRFirstMinM && K % 64 == 0 && rank % 8 == 0 &&
+      rank <= ltx25::kLoraMaxRank) {
+    // Many tokens: r = bf16(x . A^T) once with the dense GEMM (A is the
+    // [rank][K] weight of that linear), then the fused kernel's second
+    // phase reads it -- instead of recomputing x . A^T for every column
+    // split of a row block. Same roundings (r rounded once to bf16).
+    uint16_t* r = nullptr;
+    {
+      std::lock_guard<std::mutex> lk(g_mu);
+      const int rc2 = grow(&ds->lora_mm, &ds->lora_mm_bytes, (size_t)M * rank * 2);
+      if (rc2 != LTX25_OK) { return rc2; }
+      r = (uint16_t*)ds->lora_mm;
+    }
+    ltx25::GemmDesc d;
+    d.x = (const uint16_t*)x;
+    d.w = pa;
+    d.bits = 16;
+    d.group = 64;
+    d.y = r;
+    d.M = M;
+    d.N = rank;
+    d.K = K;
+    const ltx25::GemmPlan plan = ltx25::plan_gemm(M, rank, K, 16, ds->cu_count);
+    float* ws = nullptr;
+    if (plan.workspace_bytes > 0) {
+      std::lock_guard<std::mutex> lk(g_mu);
+      const int rc2 = grow(&ds->ws, &ds->ws_bytes, plan.workspace_bytes);
+      if (rc2 != LTX25_OK) { return rc2; }
+      ws = (float*)ds->ws;
+    }
+    hipError_t e = ltx25::launch_gemm(d, plan, ws, (hipStream_t)stream);
+    if (e != hipSuccess) { return hip_fail(e, "lora r gemm launch"); }
+    e = ltx25::launch_lora((const uint16_t*)x, pa, pb, (uint16_t*)y, M, K, N, rank, ldb, vec,
+                           ds->cu_count, (hipStream_t)stream, r);
+    if (e != hipSuccess) { return hip_fail(e, "lora launch"); }
+    return LTX25_OK;
   }
   for (int c = 0; c < rank; c += ltx25::kLoraMaxRank) {
     const int rp = rank - c < ltx25::kLoraMaxRank ? rank - c : ltx25::kLoraMaxRank;

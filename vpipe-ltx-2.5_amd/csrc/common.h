@@ -137,11 +137,14 @@ hipError_t launch_splitk_reduce(const float* partial, int splits, const void* bi
 // selects 16-byte operand loads (K % 8 == 0, ldb % 8 == 0, N % 8 == 0,
 // aligned pointers, every operand under 2 GiB, and B's columns zero from
 // `rank` up to the next multiple of 8).
+// With `r_in` set ([M][rank] bf16, rank % 8 == 0, vector path only) the
+// launch skips the x . A^T phase and reads r from it.
 constexpr int kLoraMaxRank = 512;
-int lora_splits(int M, int N, int rank, int cu_count);
+int lora_splits(int M, int N, int rank, int cu_count, bool pre_r);
 hipError_t launch_lora(const uint16_t* x, const uint16_t* a, const uint16_t* b,
                        uint16_t* y, int M, int K, int N, int rank, int ldb,
-                       bool vec, int cu_count, hipStream_t stream);
+                       bool vec, int cu_count, hipStream_t stream,
+                       const uint16_t* r_in = nullptr);
 // B [rows][cols] (row stride ld_src) -> [rows][ld_dst] with zero columns past
 // `cols`: the vector path's copy of an adapter whose rank is not a multiple
 // of 8.

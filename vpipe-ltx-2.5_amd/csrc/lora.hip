@@ -24,6 +24,11 @@
 //
 // The rank handled by one launch is at most kLoraMaxRank; the host runs a
 // larger adapter as several launches over column slices of A and B.
+//
+// With many tokens the host computes r = bf16(x . A^T) once with the dense
+// GEMM instead (phase 1 here re-reads x and all of A for every column split
+// of a row block) and the kernel runs phase 2 only, reading its 32 rows of
+// r from that buffer (`r_in`, [M][rank], rank % 8 == 0).
 
 #include "common.h"
 
@@ -36,6 +41,7 @@ constexpr int kLoraThreads = kLoraWaves * 64;
 constexpr int kYsRow = 128 + 8;   // bf16 per row of a y staging tile (16 B pad)
 
 struct LoraParams {
+  const uint16_t* r_in;  // precomputed r [M][rank] (phase 2 only), or null
   const uint16_t* x;
   const uint16_t* a;  // this pass's first row of A
   const uint16_t* b;  // this pass's first column of B
@@ -90,8 +96,9 @@ __device__ __forceinline__ bf16x8 frag8s(const uint16_t* p, int row, int rows, i
   return __builtin_bit_cast(bf16x8, v);
 }
 
-// RB = 32-column blocks of rank this instance covers (rank <= 32 * RB).
-template <int RB, bool VEC>
+// RB = 32-column blocks of rank this instance covers (rank <= 32 * RB);
+// PRE_R: r comes from p.r_in instead of phase 1.
+template <int RB, bool VEC, bool PRE_R>
 __global__ __launch_bounds__(kLoraThreads) void lora_kernel(LoraParams p)
 {
   constexpr int RP = 32 * RB;        // rank padded to the MFMA block
@@ -103,7 +110,8 @@ __global__ __launch_bounds__(kLoraThreads) void lora_kernel(LoraParams p)
   __shared__ __attribute__((aligned(16))) uint16_t ystage[VEC ? kLoraWaves * kLoraRows * kYsRow : 8];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform (an SGPR), so that the loop bounds below are too
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
   const int m0 = blockIdx.x * kLoraRows;
@@ -120,93 +128,111 @@ __global__ __launch_bounds__(kLoraThreads) void lora_kernel(LoraParams p)
     else { return frag8s(p.a, rb * 32 + l32, p.rank, k, p.K, p.K); }
   };
 
-  // ---- phase 1: r^T[i][m] = sum_k A[i][k] x[m][k] ---------------------------
-  // Narrow adapters (RB < 4) split K over the four waves and add the
-  // partials through LDS in wave order; wide ones split the rank blocks
-  // (RB / 4 per wave, each over all of K), so every wave owns its columns of
-  // r and no reduction is needed. Either way the K steps of 16 run through
-  // a ring of D1 register slots: slot d holds one step's fragments and is
-  // refilled with the step D1 ahead as soon as its MFMAs have been issued.
-  // A step past the end loads zeros (k = K is outside every row).
-  constexpr bool kRankSplit = RB >= 4;
-  constexpr int RBW = kRankSplit ? RB / kLoraWaves : RB;   // rank blocks per wave
-  constexpr int D1 = kRankSplit ? 4 : 8 / RB;
-  const int rb0 = kRankSplit ? wave * RBW : 0;
-  f32x16 acc[RBW];
-#pragma unroll
-  for (int rb = 0; rb < RBW; ++rb) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) { acc[rb][r] = 0.0f; }
-  }
-  const int steps = (p.K + 15) / 16;
-  const int nloc = kRankSplit ? steps : (steps - wave + kLoraWaves - 1) / kLoraWaves;
-  auto kstep = [&](int j) {
-    if (j >= nloc) { return p.K; }
-    return (kRankSplit ? j : wave + j * kLoraWaves) * 16 + hi * 8;
-  };
-  bf16x8 xf[D1];
-  bf16x8 af[D1][RBW];
-#pragma unroll
-  for (int d = 0; d < D1; ++d) {
-    const int k = kstep(d);
-    xf[d] = xfrag(k);
-#pragma unroll
-    for (int rb = 0; rb < RBW; ++rb) { af[d][rb] = afrag(rb0 + rb, k); }
-  }
-  for (int j0 = 0; j0 < nloc; j0 += D1) {
-#pragma unroll
-    for (int d = 0; d < D1; ++d) {
-      if (j0 + d >= nloc) { break; }
-      const int kn = kstep(j0 + d + D1);
-      const bf16x8 xc = xf[d];
-      xf[d] = xfrag(kn);
-#pragma unroll
-      for (int rb = 0; rb < RBW; ++rb) {
-        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[d][rb], xc, acc[rb], 0, 0, 0);
-        af[d][rb] = afrag(rb0 + rb, kn);
-      }
-    }
-  }
-
-  // Lane l, register r of block rb holds r^T[i][m] with m = l & 31 and
-  // i = 32 rb + 8 (r / 4) + 4 (l / 32) + r % 4; r lands in rl[m][i] as bf16.
-  auto put_r = [&](int rb, int g, f32x4 v) {
-    uint2 o;
-    o.x = pack_bf16x2(v[0], v[1]);
-    o.y = pack_bf16x2(v[2], v[3]);
-    *(uint2*)(rl + l32 * RS + rb * 32 + g * 8 + hi * 4) = o;
-  };
-  if constexpr (kRankSplit) {
-#pragma unroll
-    for (int rb = 0; rb < RBW; ++rb) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        put_r(rb0 + rb, g, f32x4{acc[rb][4 * g], acc[rb][4 * g + 1], acc[rb][4 * g + 2],
-                                 acc[rb][4 * g + 3]});
-      }
+  if constexpr (PRE_R) {
+    // r's rows m0..m0+31, columns 0..RP-1 (zero past rank and M) -> rl, as
+    // 16-byte chunks: rank % 8 == 0, so a chunk is wholly inside or outside
+    const auto rr = rsrc(p.r_in, (size_t)p.M * p.rank * 2);
+    constexpr int kCh = RP / 8;
+    for (int e = threadIdx.x; e < kLoraRows * kCh; e += kLoraThreads) {
+      const int row = e / kCh;
+      const int col = (e % kCh) * 8;
+      const uint32_t off = (m0 + row < p.M && col < p.rank)
+                               ? (uint32_t)((m0 + row) * p.rank + col) * 2u
+                               : kOob;
+      *(i32x4*)(rl + row * RS + col) = __builtin_amdgcn_raw_buffer_load_b128(rr, (int)off, 0, 0);
     }
     __syncthreads();
   } else {
-    // waves add in order 0..3 through LDS; the last rounds to bf16
-    for (int w = 0; w < kLoraWaves; ++w) {
-      if (wave == w) {
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            float* dst = red + l32 * FS + rb * 32 + g * 8 + hi * 4;
-            f32x4 v = {acc[rb][4 * g], acc[rb][4 * g + 1], acc[rb][4 * g + 2],
-                       acc[rb][4 * g + 3]};
-            if (w > 0) { v += *(const f32x4*)dst; }
-            if (w < kLoraWaves - 1) {
-              *(f32x4*)dst = v;
-            } else {
-              put_r(rb, g, v);
-            }
-          }
+    // ---- phase 1: r^T[i][m] = sum_k A[i][k] x[m][k] ---------------------------
+    // Narrow adapters (RB < 4) split K over the four waves and add the
+    // partials through LDS in wave order; wide ones split the rank blocks
+    // (RB / 4 per wave, each over all of K), so every wave owns its columns of
+    // r and no reduction is needed. Either way the K steps of 16 run through
+    // a ring of D1 register slots: slot d holds one step's fragments and is
+    // refilled with the step D1 ahead as soon as its MFMAs have been issued.
+    // A step past the end loads zeros (k = K is outside every row) and its
+    // MFMAs add zeros: the ring's body has no exit, so the compiler's waits
+    // stay one slot deep (an early exit from the body made it drain every
+    // load before each MFMA).
+    constexpr bool kRankSplit = RB >= 4;
+    constexpr int RBW = kRankSplit ? RB / kLoraWaves : RB;   // rank blocks per wave
+    constexpr int D1 = kRankSplit ? 4 : 8 / RB;
+    const int rb0 = kRankSplit ? wave * RBW : 0;
+    f32x16 acc[RBW];
+  #pragma unroll
+    for (int rb = 0; rb < RBW; ++rb) {
+  #pragma unroll
+      for (int r = 0; r < 16; ++r) { acc[rb][r] = 0.0f; }
+    }
+    const int steps = (p.K + 15) / 16;
+    const int nloc = kRankSplit ? steps : (steps - wave + kLoraWaves - 1) / kLoraWaves;
+    auto kstep = [&](int j) {
+      if (j >= nloc) { return p.K; }
+      return (kRankSplit ? j : wave + j * kLoraWaves) * 16 + hi * 8;
+    };
+    bf16x8 xf[D1];
+    bf16x8 af[D1][RBW];
+  #pragma unroll
+    for (int d = 0; d < D1; ++d) {
+      const int k = kstep(d);
+      xf[d] = xfrag(k);
+  #pragma unroll
+      for (int rb = 0; rb < RBW; ++rb) { af[d][rb] = afrag(rb0 + rb, k); }
+    }
+    for (int j0 = 0; j0 < nloc; j0 += D1) {
+  #pragma unroll
+      for (int d = 0; d < D1; ++d) {
+        const int kn = kstep(j0 + d + D1);
+        const bf16x8 xc = xf[d];
+        xf[d] = xfrag(kn);
+  #pragma unroll
+        for (int rb = 0; rb < RBW; ++rb) {
+          acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[d][rb], xc, acc[rb], 0, 0, 0);
+          af[d][rb] = afrag(rb0 + rb, kn);
+        }
+      }
+    }
+
+    // Lane l, register r of block rb holds r^T[i][m] with m = l & 31 and
+    // i = 32 rb + 8 (r / 4) + 4 (l / 32) + r % 4; r lands in rl[m][i] as bf16.
+    auto put_r = [&](int rb, int g, f32x4 v) {
+      uint2 o;
+      o.x = pack_bf16x2(v[0], v[1]);
+      o.y = pack_bf16x2(v[2], v[3]);
+      *(uint2*)(rl + l32 * RS + rb * 32 + g * 8 + hi * 4) = o;
+    };
+    if constexpr (kRankSplit) {
+  #pragma unroll
+      for (int rb = 0; rb < RBW; ++rb) {
+  #pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          put_r(rb0 + rb, g, f32x4{acc[rb][4 * g], acc[rb][4 * g + 1], acc[rb][4 * g + 2],
+                                   acc[rb][4 * g + 3]});
         }
       }
       __syncthreads();
+    } else {
+      // waves add in order 0..3 through LDS; the last rounds to bf16
+      for (int w = 0; w < kLoraWaves; ++w) {
+        if (wave == w) {
+  #pragma unroll
+          for (int rb = 0; rb < RB; ++rb) {
+  #pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              float* dst = red + l32 * FS + rb * 32 + g * 8 + hi * 4;
+              f32x4 v = {acc[rb][4 * g], acc[rb][4 * g + 1], acc[rb][4 * g + 2],
+                         acc[rb][4 * g + 3]};
+              if (w > 0) { v += *(const f32x4*)dst; }
+              if (w < kLoraWaves - 1) {
+                *(f32x4*)dst = v;
+              } else {
+                put_r(rb, g, v);
+              }
+            }
+          }
+        }
+        __syncthreads();
+      }
     }
   }
 
@@ -344,10 +370,12 @@ __global__ __launch_bounds__(kLoraThreads) void lora_kernel(LoraParams p)
 template <int RB>
 hipError_t launch_rb(const LoraParams& p, bool vec, dim3 grid, hipStream_t stream)
 {
-  if (vec) {
-    lora_kernel<RB, true><<<grid, kLoraThreads, 0, stream>>>(p);
+  if (p.r_in != nullptr) {
+    lora_kernel<RB, true, true><<<grid, kLoraThreads, 0, stream>>>(p);
+  } else if (vec) {
+    lora_kernel<RB, true, false><<<grid, kLoraThreads, 0, stream>>>(p);
   } else {
-    lora_kernel<RB, false><<<grid, kLoraThreads, 0, stream>>>(p);
+    lora_kernel<RB, false, false><<<grid, kLoraThreads, 0, stream>>>(p);
   }
   return hipGetLastError();
 }
@@ -399,10 +427,10 @@ hipError_t launch_lora_pad(const uint16_t* src, int rows, int cols, int ld_src, 
 // workgroups to cover the CUs once; a narrow one, whose phase 2 is bound by
 // y traffic and wants waves in flight, gets two per CU. Never fewer than
 // 1024 columns per workgroup.
-int lora_splits(int M, int N, int rank, int cu_count)
+int lora_splits(int M, int N, int rank, int cu_count, bool pre_r)
 {
   const int mtiles = (M + kLoraRows - 1) / kLoraRows;
-  const int per_cu = rank > 128 ? 1 : 2;
+  const int per_cu = rank > 128 && !pre_r ? 1 : 2;
   const int want = per_cu * cu_count / mtiles;
   const int cap = (N + 1023) / 1024;
   return want < 1 ? 1 : (want < cap ? want : cap);
@@ -410,16 +438,17 @@ int lora_splits(int M, int N, int rank, int cu_count)
 
 hipError_t launch_lora(const uint16_t* x, const uint16_t* a, const uint16_t* b,
                        uint16_t* y, int M, int K, int N, int rank, int ldb,
-                       bool vec, int cu_count, hipStream_t stream)
+                       bool vec, int cu_count, hipStream_t stream, const uint16_t* r_in)
 {
   if (rank <= 0 || rank > kLoraMaxRank) { return hipErrorInvalidValue; }
-  const int splits = lora_splits(M, N, rank, cu_count);
+  if (r_in != nullptr && (!vec || rank % 8 != 0)) { return hipErrorInvalidValue; }
+  const int splits = lora_splits(M, N, rank, cu_count, r_in != nullptr);
   int n_split = (N + splits - 1) / splits;
   // whole super-block strides (4 waves x 128 columns) where N allows
   const int quantum = N >= 512 ? 512 : 32;
   n_split = (n_split + quantum - 1) / quantum * quantum;
   const int gy = (N + n_split - 1) / n_split;
-  LoraParams p{x, a, b, y, M, K, N, rank, ldb, n_split};
+  LoraParams p{r_in, x, a, b, y, M, K, N, rank, ldb, n_split};
   const dim3 grid((unsigned)((M + kLoraRows - 1) / kLoraRows), (unsigned)gy);
   const int rb = (rank + 31) / 32;
   if (rb <= 1) { return launch_rb<1>(p, vec, grid, stream); }
