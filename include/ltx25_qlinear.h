@@ -177,12 +177,15 @@ int ltx25_dequant_once_takes(int M, int K, int N);
 
 /* y[M][N] += (x[M][K] . a[rank][K]^T) . b[N][rank]^T, all bf16, in place on
  * y: r = bf16(x . a^T) with f32 accumulation, then y = bf16(f32(y) + r . b^T)
- * with the accumulator seeded from y. Two routes, same arithmetic:
+ * with the accumulator seeded from y. Three routes, same arithmetic:
  * - rank >= 96, M >= 256, K % 64 == 0, N % 8 == 0, 16-byte aligned x and y:
  *   the reference's matrix-core pair -- r on the dense GEMM, then the dense
  *   GEMM again with its accumulators seeded from y; the rank is padded to a
  *   multiple of 64 (a and b copied with zero rows / columns when needed) in
  *   a grow-only scratch that also holds r;
+ * - rank < 96 with M >= 512, K % 64 == 0, rank % 8 == 0 and the vector
+ *   path's conditions (below): r on the dense GEMM into that scratch, then
+ *   the fused kernel's y pass reading it;
  * - otherwise one fused kernel per 512 adapter columns (16-byte aligned x,
  *   a and y with K % 8 == 0 and N % 8 == 0 take its vector path; when the
  *   rank is not a multiple of 8, b is first copied with its rows
