@@ -1,7 +1,7 @@
 """The M <= 128 route (skinny.hip) on the GPU, through the C ABI.
 
-Every linear with at most 128 tokens takes this kernel: 32 output columns per
-workgroup, the workgroup's K (up to 2048) split between its 8 waves in runs
+A linear with at most 128 tokens takes this kernel unless its weight is large
+enough to need more than 3 workgroups per CU: 32 output columns per workgroup, the workgroup's K (up to 2048) split between its 8 waves in runs
 of 64-wide chunks, split-K across workgroups above 2048. Its lane mapping
 (X chunks swizzled in LDS, a permuted K order shared by both operands, the
 codes transposed through LDS, the cross-wave sum) is pinned two ways:

@@ -121,8 +121,8 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
                        float* workspace, hipStream_t stream);
 // The M <= 128 route (skinny.hip): 32 output columns per workgroup, K split
 // between its 8 waves, and across workgroups above 2048. Fills `plan` and
-// returns true when it takes the shape.
-bool plan_skinny(int M, int N, int K, int bits, GemmPlan& plan);
+// returns true when it takes the shape (up to 3 workgroups per CU).
+bool plan_skinny(int M, int N, int K, int bits, int cu_count, GemmPlan& plan);
 hipError_t launch_skinny(const GemmDesc& d, const GemmPlan& plan, float* workspace,
                          hipStream_t stream);
 // Sums `splits` f32 partial planes [M][N] in split order, adds bias and

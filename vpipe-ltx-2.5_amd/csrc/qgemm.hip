@@ -734,7 +734,7 @@ int ilog2(int v)
 GemmPlan plan_gemm(int M, int N, int K, int bits, int cu_count)
 {
   GemmPlan plan;
-  if (plan_skinny(M, N, K, bits, plan)) { return plan; }
+  if (plan_skinny(M, N, K, bits, cu_count, plan)) { return plan; }
   const long tall_tiles = (long)((M + 255) / 256) * ((N + 255) / 256);
   if (M > 128 && tall_tiles >= cu_count) {
     plan.tile = 0;

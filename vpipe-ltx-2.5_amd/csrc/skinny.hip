@@ -1,5 +1,6 @@
 // The quantized linear for at most 128 tokens on gfx950 -- the audio
-// stream's GEMMs (126 tokens) and any other call with M <= 128:
+// stream's GEMMs (126 tokens) and any other call with M <= 128 whose weight
+// needs at most 3 workgroups per CU (larger ones run on the 128 x 128 tile):
 // y = x . dequant(W)^T (+ bias) (+ GELU) (+ y_in).
 //
 // At these shapes the activation slab X [M][K] is small (516 KB at
@@ -438,7 +439,7 @@ skinny_kernel(SParams p)
 
 }  // namespace
 
-bool plan_skinny(int M, int N, int K, int bits, GemmPlan& plan)
+bool plan_skinny(int M, int N, int K, int bits, int cu_count, GemmPlan& plan)
 {
   constexpr size_t kTwoGib = (size_t)1 << 31;
   if (M < 1 || M > kRows || (bits != 8 && bits != 4 && bits != 16) || K < kChunk ||
@@ -451,6 +452,11 @@ bool plan_skinny(int M, int N, int K, int bits, GemmPlan& plan)
   int s = (chunks + kPerGroup - 1) / kPerGroup;
   const int per = (chunks + s - 1) / s;
   s = (chunks + per - 1) / per;
+  // Every 32-column workgroup reads all of X from L2: past about three
+  // workgroups per CU (a large N x K weight) that stream costs more than the
+  // 128 x 128 tile's partials (measured, M = 16..126: that tile is faster
+  // from 1024 workgroups, e.g. 62 vs 72 us at K = 4096, N = 16384).
+  if ((long)((N + kCols - 1) / kCols) * s > 3L * cu_count) { return false; }
   plan.tile = 2;
   plan.splits = s;
   plan.k_chunk = per * kChunk;
