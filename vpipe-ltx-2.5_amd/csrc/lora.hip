@@ -254,7 +254,10 @@ __global__ __launch_bounds__(kLoraThreads) void lora_kernel(LoraParams p)
     constexpr int KS = 2 * RB;                      // 16-deep rank steps
     constexpr int kSb = 4;                          // MFMA blocks per super block
     constexpr int kSbStride = kLoraWaves * kSb * 32;
-    constexpr int kDy = 2;
+    // Four super blocks of y in flight for ranks up to 64 (5-7 us less on
+    // an 8160 x 16384 y at ranks 8-64); above that the two extra slots'
+    // 32 VGPRs each would halve the waves per SIMD, so two.
+    constexpr int kDy = RB <= 2 ? 4 : 2;
     // B's rows are zero-padded to a multiple of 8 (the host pads a copy when
     // the adapter's rank is not), so an 8-column chunk below rank8 is whole.
     const int rank8 = (p.rank + 7) & ~7;
