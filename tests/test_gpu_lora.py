@@ -51,6 +51,10 @@ SHAPES = [
     ("r first: rank 32 at the FFN width", 1024, 4096, 16384, 32),
     ("r first: rank 40, ragged M", 777, 1024, 2048, 40),
     ("r first: rank 8", 600, 512, 1024, 8),
+    # N not a multiple of the 512-column super-block stride: the y loads issued four
+    # super blocks ahead (ranks up to 64) run past the column split's end
+    ("r first: rank 16, ragged N", 640, 1024, 1000, 16),
+    ("r first: rank 64, N = 4104", 520, 256, 4104, 64),
 ]
 
 
