@@ -170,8 +170,49 @@ int ltx25_dequant(void* stream, const ltx25_qweight* w, void* out_bf16,
 int ltx25_set_dequant_once(int mode);
 
 /* 1 when ltx25_linear_q would take the dequant-once arm for this shape
- * under the current mode (K must also be a multiple of 64). Host-only. */
+ * under the current mode (K must also be a multiple of 64; the bf16
+ * expansion must stay under 2 GiB). Host-only. */
 int ltx25_dequant_once_takes(int M, int K, int N);
+
+/* ---- routing: what a linear runs on, and the A/B switch ------------------------ */
+
+/* Tile families of the GEMM behind ltx25_linear / ltx25_linear_q:
+ *   TALL    256 x 256 output tiles, all of K per workgroup (the video GEMMs)
+ *   MID     128 x 128 tiles, K split across workgroups until they cover the
+ *           CUs once, f32 partials summed in split order by a second launch
+ *   SKINNY  at most 128 tokens: 32-column slices, K split between the 8
+ *           waves (and across workgroups above K = 2048)
+ * ltx25_set_tile forces one for every later linear (AUTO restores the
+ * planner); a forced SKINNY falls back to the planner for shapes it cannot
+ * take (M > 128). Results are deterministic for a given route; different
+ * routes sum in different orders. Process-wide, like the reference's
+ * VPIPE_LTX25_MMA_TILE override (src/ltx25-metal-ops.cc:193-231, read at
+ * init there), which exists for the same A/B re-measurement. */
+#define LTX25_TILE_AUTO 0
+#define LTX25_TILE_TALL 1
+#define LTX25_TILE_MID 2
+#define LTX25_TILE_SKINNY 3
+int ltx25_set_tile(int tile);
+
+/* The route ltx25_linear_q (bits 4 / 8) or ltx25_linear (bits 16) takes
+ * for a shape under the current switches. Host-only, no device use. */
+typedef struct ltx25_route {
+  int tile;            /* LTX25_TILE_TALL / MID / SKINNY; 0 for the int8 tier */
+  int i8;              /* 1: the int8 tier (ltx25_set_i8_gemm) */
+  int dequant_once;    /* 1: the weight is expanded to bf16 first */
+  int splits;          /* split-K factor of each launch */
+  int slabs;           /* launches over row slabs */
+  int slab_rows;       /* rows per slab (M when one) */
+  size_t scratch_bytes;/* library scratch the call uses */
+} ltx25_route;
+
+/* Operand size limit: the kernels address every operand with 32-bit buffer
+ * offsets, so each operand of a launch must stay under 2 GiB. The
+ * activation and output are cut into row slabs (multiples of 256 rows)
+ * that do; a weight of 2 GiB or more is refused with LTX25_E_UNSUPPORTED
+ * before any device use. The reference refuses the same operands for the
+ * same reason (mma_eligible_, src/ltx25-metal-ops.cc:342-374). */
+int ltx25_linear_route(int M, int K, int N, int bits, ltx25_route* out);
 
 /* ---- the low-rank adapter delta ------------------------------------------------ */
 
@@ -199,11 +240,36 @@ int ltx25_dequant_once_takes(int M, int K, int N);
 int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
                    void* y, void* r, void* d, int M, int K, int N, int rank);
 
-/* 1 when ltx25_lora_add runs this shape on the MFMA kernel: every
- * non-empty shape does (there is no portable fallback on gfx950); 0 for an
- * empty one. Replaces MetalOps::lora_on_matrix_cores
- * (src/ltx25-metal-ops.h:134-139). Host-only. */
+/* The three LoRA routes (see ltx25_lora_add); NONE for an empty shape. */
+#define LTX25_LORA_AUTO 0
+#define LTX25_LORA_NONE 0
+#define LTX25_LORA_PAIR 1    /* two dense GEMMs, the second seeded from y */
+#define LTX25_LORA_RFIRST 2  /* r on the dense GEMM, then the fused y pass */
+#define LTX25_LORA_FUSED 3   /* one fused kernel per 512 adapter columns */
+
+/* 1 when ltx25_lora_add takes the GEMM pair for this shape (with
+ * allocator-aligned pointers) under the current switches, else 0.
+ * Replaces MetalOps::lora_on_matrix_cores (src/ltx25-metal-ops.h:134-139;
+ * src/ltx25-metal-ops.cc:921-936). Host-only. */
 int ltx25_lora_on_matrix_cores(int M, int K, int N, int rank);
+
+/* Turn the GEMM pair off (0: every shape takes the one-pass fused kernel)
+ * or back on (1: the planner's choice). The A/B hook of
+ * MetalOps::set_lora_matrix_cores (src/ltx25-metal-ops.h:140-146).
+ * Process-wide. */
+int ltx25_set_lora_matrix_cores(int on);
+
+/* Force one LoRA route for every later ltx25_lora_add (LTX25_LORA_AUTO
+ * restores the planner). A forced route that cannot take a shape makes
+ * that call fail with LTX25_E_UNSUPPORTED before any device use; FUSED
+ * takes every shape. Process-wide. */
+int ltx25_set_lora_route(int route);
+
+/* The route ltx25_lora_add would take for these pointers and shape under
+ * the current switches, in *route (LTX25_LORA_*). Pointers are only
+ * inspected (alignment), never dereferenced. Host-only. */
+int ltx25_lora_route(const void* x, const void* a, const void* b, const void* y, int M, int K,
+                     int N, int rank, int* route);
 
 /* ---- the int8 tier ------------------------------------------------------------ */
 
@@ -212,7 +278,10 @@ int ltx25_lora_on_matrix_cores(int M, int K, int N, int rank);
 int ltx25_set_i8_gemm(int on);
 
 /* 1 when linear would take the int8 tier for this shape: the tier is on,
- * M >= 1024, K >= 1024, K % 128 == 0 and N >= 16. Host-only, no device use.
+ * M >= 1024, K >= 1024, K % 128 == 0, N >= 16, and the int8 operands and
+ * the output stay under 2 GiB. The tier composes with the GELU epilogue
+ * (ltx25_linear_q_ex), as the reference's tier sits under every quantized
+ * linear, ff_in included. Host-only, no device use.
  * Replaces MetalOps::i8_takes (src/ltx25-metal-ops.h:157; the reference's
  * gates are asserted at tests/ltx25-i8-gemm-test.cc:144-179). */
 int ltx25_i8_takes(int M, int K, int N);

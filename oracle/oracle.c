@@ -404,6 +404,32 @@ void orc_i8_epilogue(const int32_t* acc, const float* sx, const float* sw,
   }
 }
 
+/* orc_i8_epilogue followed by the feed-forward's GELU-tanh (epilogue 1)
+ * before the one rounding: y = bf16(gelu(fma(float(acc), sx[m] * sw[n],
+ * bias[n]))), gelu as orc_gelu_tanh. epilogue 0 is orc_i8_epilogue. The
+ * composition the int8 tier computes under ff_in (src/ltx25-block-metal.cc:
+ * 639-645 runs linear then gelu; the tier sits under that linear,
+ * src/ltx25-metal-ops.cc:376-391). */
+void orc_i8_epilogue_ex(const int32_t* acc, const float* sx, const float* sw,
+                        const void* bias, int bias_dtype, int epilogue, int M, int N,
+                        uint16_t* y)
+{
+  for (int m = 0; m < M; ++m) {
+    for (int n = 0; n < N; ++n) {
+      float b = 0.0f;
+      if (bias != NULL && bias_dtype == 1) {
+        b = orc_bf16_to_f32(((const uint16_t*)bias)[n]);
+      } else if (bias != NULL && bias_dtype == 2) {
+        b = ((const float*)bias)[n];
+      }
+      const float sc = sx[m] * sw[n];
+      float v = fmaf((float)acc[(size_t)m * N + n], sc, b);
+      if (epilogue == 1) { orc_gelu_tanh(&v, &v, 1); }
+      y[(size_t)m * N + n] = orc_bf16_rne(v);
+    }
+  }
+}
+
 /* splitmix64 stream + Box-Muller in double: a seeded N(mean, stddev)
  * generator whose output does not depend on the C library. */
 static uint64_t splitmix64(uint64_t* s)

@@ -42,6 +42,9 @@
  *   orc_i8_quantize_rows             numpy rint / absmax closed form
  *   orc_i8_gemm_i32                  numpy int64 matmul
  *   orc_i8_epilogue                  closed form via numpy float32 fma
+ *   orc_i8_epilogue_ex               epilogue 0 equals orc_i8_epilogue; epilogue 1
+ *                                    equals orc_i8_epilogue's f32 value through
+ *                                    orc_gelu_tanh, then one bf16 rounding
  * Not pinned against the reference: the exact output bits of libvpipe's
  * GEMM kernels and of its I8GemmContext (not present in the reference
  * tree), so parity there is against the closed-form semantics above.
@@ -97,6 +100,9 @@ void orc_i8_gemm_i32(const int8_t* xq, const int8_t* wq, int M, int K, int N,
 void orc_i8_epilogue(const int32_t* acc, const float* sx, const float* sw,
                      const void* bias, int bias_dtype, int M, int N,
                      uint16_t* y);
+void orc_i8_epilogue_ex(const int32_t* acc, const float* sx, const float* sw,
+                        const void* bias, int bias_dtype, int epilogue, int M, int N,
+                        uint16_t* y);
 
 /* ---- seeded synthetic data --------------------------------------------- */
 void orc_fill_normal(float* out, size_t n, uint64_t seed, float mean,

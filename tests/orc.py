@@ -41,6 +41,7 @@ _SIGS = {
     "orc_i8_quantize_rows": (None, [_vp, _i, _i, _vp, _vp]),
     "orc_i8_gemm_i32": (None, [_vp, _vp, _i, _i, _i, _vp]),
     "orc_i8_epilogue": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "orc_i8_epilogue_ex": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "orc_fill_normal": (None, [_vp, _sz, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
 }
 
@@ -244,7 +245,7 @@ def i8_gemm_i32(xq, wq) -> np.ndarray:
     return acc
 
 
-def i8_epilogue(acc, sx, sw, bias=None, bias_dtype=0) -> np.ndarray:
+def i8_epilogue(acc, sx, sw, bias=None, bias_dtype=0, epilogue=0) -> np.ndarray:
     acc = _c(acc, np.int32)
     sx = _c(sx, np.float32)
     sw = _c(sw, np.float32)
@@ -252,7 +253,11 @@ def i8_epilogue(acc, sx, sw, bias=None, bias_dtype=0) -> np.ndarray:
     if bias is not None:
         bias = _c(bias, np.uint16 if bias_dtype == 1 else np.float32)
     y = np.empty((M, N), np.uint16)
-    lib().orc_i8_epilogue(_p(acc), _p(sx), _p(sw), _p(bias), bias_dtype, M, N, _p(y))
+    if epilogue == 0:
+        lib().orc_i8_epilogue(_p(acc), _p(sx), _p(sw), _p(bias), bias_dtype, M, N, _p(y))
+    else:
+        lib().orc_i8_epilogue_ex(_p(acc), _p(sx), _p(sw), _p(bias), bias_dtype, epilogue, M, N,
+                                 _p(y))
     return y
 
 

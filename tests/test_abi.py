@@ -94,10 +94,19 @@ def test_dequant_once_and_lora_gates(pkg, lib):
         assert lib.ltx25_set_dequant_once(7) == pkg.E_INVAL
     finally:
         pkg.set_dequant_once(pkg.DEQUANT_ONCE_AUTO)
-    assert pkg.lora_on_matrix_cores(128, 4096, 16384, 32)
-    assert pkg.lora_on_matrix_cores(64, 1024, 1024, 450)
+    # the GEMM pair from rank 96 and 256 tokens (the reference's matrix-core pair)
+    assert pkg.lora_on_matrix_cores(8160, 4096, 16384, 450)
+    assert pkg.lora_on_matrix_cores(256, 1024, 1024, 96)
+    assert not pkg.lora_on_matrix_cores(8160, 4096, 16384, 32)   # one-pass kernel
+    assert not pkg.lora_on_matrix_cores(255, 1024, 1024, 450)
     assert not pkg.lora_on_matrix_cores(0, 64, 64, 3)
     assert not pkg.lora_on_matrix_cores(12, 64, 64, 0)
+    try:
+        pkg.set_lora_matrix_cores(False)
+        assert not pkg.lora_on_matrix_cores(8160, 4096, 16384, 450)
+    finally:
+        pkg.set_lora_matrix_cores(True)
+    assert pkg.lora_on_matrix_cores(8160, 4096, 16384, 450)
 
 
 def test_lora_validation_precedes_any_device_use(pkg, lib):
@@ -153,3 +162,106 @@ def test_cpp_facade_compiles():
                         "-I" + os.path.join(ROOT, "vpipe-ltx-2.5_amd", "csrc")],
                        input=src, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-2000:]
+
+
+class _Fake:
+    """Stands in for a tensor in the host-only route queries: only the
+    address is read (for alignment), never dereferenced."""
+
+    def __init__(self, addr):
+        self.addr = addr
+
+    def data_ptr(self):
+        return self.addr
+
+
+def test_lora_route_query_and_forcing(pkg):
+    al, odd = _Fake(0x10000), _Fake(0x10002)
+    r = lambda M, K, N, rank, x=al, a=al, b=al, y=al: pkg.lora_route(x, a, b, y, M, K, N, rank)  # noqa: E731
+    assert r(8160, 4096, 16384, 450) == pkg.LORA_PAIR
+    assert r(8160, 4096, 16384, 32) == pkg.LORA_RFIRST
+    assert r(511, 4096, 16384, 32) == pkg.LORA_FUSED             # too few tokens for r-first
+    assert r(8160, 4096, 16384, 36) == pkg.LORA_FUSED            # rank not a multiple of 8
+    assert r(8160, 4096, 16384, 32, x=odd) == pkg.LORA_FUSED     # scalar path
+    assert r(8160, 4096, 16384, 450, y=odd) == pkg.LORA_FUSED    # pair needs aligned x, y
+    assert r(0, 4096, 16384, 32) == pkg.LORA_NONE
+    try:
+        pkg.set_lora_route(pkg.LORA_FUSED)
+        assert r(8160, 4096, 16384, 450) == pkg.LORA_FUSED
+        pkg.set_lora_route(pkg.LORA_PAIR)
+        assert r(64, 4096, 1024, 16) == pkg.LORA_PAIR
+        with pytest.raises(pkg.Ltx25Error) as e:
+            r(64, 100, 1024, 16)                                  # K % 64 != 0
+        assert e.value.code == pkg.E_UNSUPPORTED
+        pkg.set_lora_route(pkg.LORA_RFIRST)
+        assert r(64, 4096, 1024, 16) == pkg.LORA_RFIRST
+        with pytest.raises(pkg.Ltx25Error):
+            r(64, 4096, 1024, 12)                                 # rank % 8 != 0
+        import ctypes
+        lib = pkg.load()
+        # a forced route that cannot take the shape fails before any device use
+        assert lib.ltx25_lora_add(None, 0x10000, 0x10000, 0x10000, 0x10000, None, None, 64, 4096,
+                                  1024, 12) == pkg.E_UNSUPPORTED
+        assert lib.ltx25_set_lora_route(9) == pkg.E_INVAL
+        del ctypes
+    finally:
+        pkg.set_lora_route(pkg.LORA_AUTO)
+
+
+def test_linear_route_and_tile_switch(pkg, lib):
+    r = pkg.linear_route
+    # the video GEMMs fill 256 CUs with 256 x 256 tiles; the audio ones take the M <= 128 kernel
+    assert r(8160, 4096, 16384)["tile"] == pkg.TILE_TALL
+    assert r(8160, 4096, 16384)["dequant_once"] == 1
+    assert r(126, 2048, 6144)["tile"] == pkg.TILE_SKINNY
+    assert r(126, 8192, 2048)["splits"] > 1
+    assert r(320, 4096, 4096)["tile"] == pkg.TILE_MID
+    assert r(1024, 4096, 8192, bits=16)["dequant_once"] == 0
+    try:
+        pkg.set_tile(pkg.TILE_MID)
+        assert r(8160, 4096, 16384)["tile"] == pkg.TILE_MID
+        pkg.set_tile(pkg.TILE_TALL)
+        assert r(126, 2048, 6144)["tile"] == pkg.TILE_TALL
+        assert r(126, 2048, 6144)["splits"] == 1
+        pkg.set_tile(pkg.TILE_SKINNY)
+        assert r(126, 2048, 6144)["tile"] == pkg.TILE_SKINNY
+        assert r(8160, 4096, 4096)["tile"] == pkg.TILE_TALL       # SKINNY cannot take M > 128
+        assert lib.ltx25_set_tile(7) == pkg.E_INVAL
+    finally:
+        pkg.set_tile(pkg.TILE_AUTO)
+
+
+def test_operand_limit_slabs_and_refusal(pkg, lib):
+    """Every operand of a launch stays under 2 GiB (32-bit buffer offsets,
+    the reference's own limit, src/ltx25-metal-ops.cc:342-374): X and Y
+    are cut into row slabs; a weight at the limit is refused before any
+    device use."""
+    import ctypes
+
+    r = pkg.linear_route
+    assert r(8160, 4096, 16384)["slabs"] == 1
+    big = r(300000, 4096, 4096, bits=16)        # X is 2.46 GB
+    assert big["slabs"] == 2
+    assert big["slab_rows"] % 256 == 0
+    assert big["slab_rows"] * 4096 * 2 < 2 ** 31
+    assert big["slab_rows"] * 2 >= 300000
+    # the bf16 expansion of a 2^31-byte weight would not fit: the fused kernel instead
+    assert r(8160, 65536, 16384)["dequant_once"] == 0            # w8 codes 1 GiB, bf16 2 GiB
+    with pytest.raises(pkg.Ltx25Error) as e:
+        r(8160, 32768, 65536)                                    # w8 codes exactly 2 GiB
+    assert e.value.code == pkg.E_UNSUPPORTED and "2 GiB" in str(e.value)
+    fake = 0x10000
+    q = pkg.QWeightC(None, fake, fake, fake, 8, 64, 1)
+    assert lib.ltx25_linear_q_ex(None, fake, ctypes.byref(q), None, 0, fake, 8160, 32768, 65536,
+                                 0) == pkg.E_UNSUPPORTED
+    assert "2 GiB" in pkg.last_error()
+    dense = lib.ltx25_linear(None, fake, fake, None, 0, fake, 64, 32768, 32768)   # bf16 W 2 GiB
+    assert dense == pkg.E_UNSUPPORTED
+    # the int8 tier declines operands it cannot address
+    pkg.set_i8_gemm(True)
+    try:
+        assert pkg.i8_takes(8160, 4096, 16384)
+        assert not pkg.i8_takes(600000, 4096, 4096)              # int8 X 2.46 GB
+        assert r(8160, 4096, 16384)["i8"] == 1
+    finally:
+        pkg.set_i8_gemm(False)

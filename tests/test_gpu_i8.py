@@ -176,3 +176,65 @@ def test_tier_inside_linear(pkg, name, M, K, N, want):
         assert 1e-5 < r < 3e-2, f"rel-L2 {r:.3e}"
     else:
         assert r == 0.0
+
+
+def test_tier_with_gelu_epilogue_bit_exact_accumulators(pkg):
+    """linear_q_ex with the GELU epilogue takes the tier (the reference's tier sits under
+    ff_in too, src/ltx25-metal-ops.cc:376-391): the tier's own operands re-derived by the
+    oracle give the same int32 products, and the output is the oracle's epilogue + GELU
+    within one bf16 ulp (the kernel's GELU uses the hardware exp2 / reciprocal)."""
+    M, K, N = 1024, 1024, 320
+    say(f"i8 tier + GELU inside linear_q_ex {M}x{K}->{N}")
+    rng = np.random.default_rng(36)
+    x_bits = orc.bf16_rne(rng_normal(rng, (M, K)))
+    qw, codes, scales, biases, wb = make_qweight(pkg, rng_normal(rng, (N, K), 0.02))
+    bias = rng_normal(rng, (N,), 0.01)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    pkg.set_i8_gemm(True)
+    try:
+        assert pkg.i8_takes(M, K, N)
+        assert pkg.linear_route(M, K, N)["i8"] == 1
+        pkg.linear_q(dev_bf16(x_bits), qw, dev_f32(bias), y, M, K, N, pkg.EPI_GELU_TANH)
+        torch.cuda.synchronize()
+    finally:
+        pkg.set_i8_gemm(False)
+    xq, sx = orc.i8_quantize_rows(x_bits)
+    wq, sw = orc.i8_quantize_rows(wb)
+    acc = orc.i8_gemm_i32(xq, wq)
+    want = orc.bf16_to_f32(orc.i8_epilogue(acc, sx, sw, bias, 2, epilogue=1))
+    got = host_f32(y)
+    ulp = np.abs(want) * 2.0 ** -7
+    assert np.all(np.abs(got - want) <= np.maximum(ulp, 1e-6))
+    # GELU was applied: the no-epilogue tier output differs on negative values
+    plain = orc.bf16_to_f32(orc.i8_epilogue(acc, sx, sw, bias, 2))
+    assert np.mean(np.abs(got - plain) > 0) > 0.3
+
+
+def test_tier_with_gelu_at_the_ffn_shape(pkg):
+    """8160 x 4096 -> 16384 with GELU, tier on: the route says int8, and the result is
+    within the tier's stated band of the bf16 route's (tests/ltx25-i8-gemm-test.cc:207-215)."""
+    M, K, N = 8160, 4096, 16384
+    say(f"i8 tier + GELU at the FFN shape {M}x{K}->{N}")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(37)
+    x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), device="cuda", generator=g) * 0.02
+    codes = torch.empty((N, K), dtype=torch.uint8, device="cuda")
+    sc = torch.empty((N, K // 64), dtype=torch.bfloat16, device="cuda")
+    qb = torch.empty((N, K // 64), dtype=torch.bfloat16, device="cuda")
+    pkg.quantize_affine(w, codes, sc, qb, N, K, 8, 64)
+    del w
+    qw = pkg.QWeight(codes, sc, qb, 8, 64)
+    base = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    tier = torch.empty_like(base)
+    pkg.linear_q(x, qw, None, base, M, K, N, pkg.EPI_GELU_TANH)
+    pkg.set_i8_gemm(True)
+    try:
+        assert pkg.i8_takes(M, K, N)
+        assert pkg.linear_route(M, K, N)["i8"] == 1
+        pkg.linear_q(x, qw, None, tier, M, K, N, pkg.EPI_GELU_TANH)
+        torch.cuda.synchronize()
+    finally:
+        pkg.set_i8_gemm(False)
+    r = ((tier.float() - base.float()).norm() / base.float().norm()).item()
+    assert 1e-5 < r < 3e-2, f"rel-L2 {r:.3e}"

@@ -25,36 +25,37 @@ pytestmark = pytest.mark.gpu
 MAX_REL = 1e-2   # normwise max relative error vs the oracle
 REL_L2 = 2e-2    # the reference's bar (tests/ltx25-lora-apply-test.cc:456-465)
 
-SHAPES = [
-    ("square self-attention projection", 12, 64, 64, 3),
-    ("cross-attention key (narrow in)", 8, 32, 64, 3),
-    ("cross-attention key (wide in)", 12, 64, 32, 3),
-    ("the per-head gate (4 columns out)", 12, 64, 4, 3),
-    ("the feed-forward widening", 12, 64, 256, 5),
-    ("rank 1", 6, 64, 64, 1),
-    ("x2 upscaler: attn projection", 128, 4096, 4096, 32),
-    ("x2 upscaler: ff widening", 128, 4096, 16384, 32),
-    ("distilled adapter: rank 450", 64, 1024, 1024, 450),
+F, RF, P = "fused", "rfirst", "pair"
+SHAPES = [  # name, M, K, N, rank, the route AUTO takes
+    ("square self-attention projection", 12, 64, 64, 3, F),
+    ("cross-attention key (narrow in)", 8, 32, 64, 3, F),
+    ("cross-attention key (wide in)", 12, 64, 32, 3, F),
+    ("the per-head gate (4 columns out)", 12, 64, 4, 3, F),
+    ("the feed-forward widening", 12, 64, 256, 5, F),
+    ("rank 1", 6, 64, 64, 1, F),
+    ("x2 upscaler: attn projection", 128, 4096, 4096, 32, F),
+    ("x2 upscaler: ff widening", 128, 4096, 16384, 32, F),
+    ("distilled adapter: rank 450", 64, 1024, 1024, 450, F),
     # beyond the reference's table
-    ("odd K, odd N (element-wise loads)", 45, 37, 30, 6),
-    ("video tokens, rank 64", 1000, 512, 768, 64),
-    ("two launches (rank 600)", 70, 256, 192, 600),
-    ("two launches, padded rank (530)", 96, 256, 320, 530),
-    ("N not a multiple of 8 (element-wise y)", 40, 128, 4100, 16),
-    # the GEMM pair (M >= 256, rank >= 64): rank padded to 64 with zero rows / columns
-    ("GEMM pair, rank 128, no padding", 300, 2048, 1024, 128),
-    ("GEMM pair, rank 450 padded to 512", 512, 1024, 2048, 450),
-    ("GEMM pair, ragged M and N", 777, 512, 1000, 200),
-    ("GEMM pair, rank 1000 (split-K second GEMM)", 256, 512, 640, 1000),
+    ("odd K, odd N (element-wise loads)", 45, 37, 30, 6, F),
+    ("video tokens, rank 64", 1000, 512, 768, 64, RF),
+    ("two launches (rank 600)", 70, 256, 192, 600, F),
+    ("two launches, padded rank (530)", 96, 256, 320, 530, F),
+    ("N not a multiple of 8 (element-wise y)", 40, 128, 4100, 16, F),
+    # the GEMM pair (M >= 256, rank >= 96): rank padded to 64 with zero rows / columns
+    ("GEMM pair, rank 128, no padding", 300, 2048, 1024, 128, P),
+    ("GEMM pair, rank 450 padded to 512", 512, 1024, 2048, 450, P),
+    ("GEMM pair, ragged M and N", 777, 512, 1000, 200, P),
+    ("GEMM pair, rank 1000 (split-K second GEMM)", 256, 512, 640, 1000, P),
     # r first (M >= 512, rank % 8 == 0, rank < 96): r = x . A^T by the dense GEMM, then the
     # fused kernel's second phase reads it
-    ("r first: rank 32 at the FFN width", 1024, 4096, 16384, 32),
-    ("r first: rank 40, ragged M", 777, 1024, 2048, 40),
-    ("r first: rank 8", 600, 512, 1024, 8),
+    ("r first: rank 32 at the FFN width", 1024, 4096, 16384, 32, RF),
+    ("r first: rank 40, ragged M", 777, 1024, 2048, 40, RF),
+    ("r first: rank 8", 600, 512, 1024, 8, RF),
     # N not a multiple of the 512-column super-block stride: the y loads issued four
     # super blocks ahead (ranks up to 64) run past the column split's end
-    ("r first: rank 16, ragged N", 640, 1024, 1000, 16),
-    ("r first: rank 64, N = 4104", 520, 256, 4104, 64),
+    ("r first: rank 16, ragged N", 640, 1024, 1000, 16, RF),
+    ("r first: rank 64, N = 4104", 520, 256, 4104, 64, RF),
 ]
 
 
@@ -71,13 +72,14 @@ def max_rel(got, ref):
     return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
 
 
-@pytest.mark.parametrize("what,M,K,N,rank", SHAPES, ids=[s[0] for s in SHAPES])
-def test_lora_add_against_oracle_and_f64(pkg, dev, what, M, K, N, rank):
+ROUTE = {F: 3, RF: 2, P: 1}   # LTX25_LORA_FUSED / _RFIRST / _PAIR
+
+
+def run_and_check(pkg, what, M, K, N, rank):
     x, a, b, y0 = draws(what, M, K, N, rank)
     xb, ab, bb, yb = (orc.bf16_rne(t) for t in (x, a, b, y0))
     xd, ad, bd, yd = (dev_bf16(t) for t in (xb, ab, bb, yb))
-    say(f"lora_add {what}: M={M} K={K} N={N} rank={rank}")
-    assert pkg.lora_on_matrix_cores(M, K, N, rank)
+    route = pkg.lora_route(xd, ad, bd, yd, M, K, N, rank)
     pkg.lora_add(xd, ad, bd, yd, M, K, N, rank)
     torch.cuda.synchronize()
     got = orc.bf16_to_f32(host_bits(yd))
@@ -87,6 +89,41 @@ def test_lora_add_against_oracle_and_f64(pkg, dev, what, M, K, N, rank):
     assert orc.rel_l2(got, want) < REL_L2, what
     # and it ADDED: y changed where the delta is not negligible
     assert not np.array_equal(host_bits(yd), yb)
+    return route
+
+
+@pytest.mark.parametrize("what,M,K,N,rank,route", SHAPES, ids=[s[0] for s in SHAPES])
+def test_lora_add_against_oracle_and_f64(pkg, dev, what, M, K, N, rank, route):
+    say(f"lora_add {what}: M={M} K={K} N={N} rank={rank}")
+    assert pkg.lora_on_matrix_cores(M, K, N, rank) == (route == P)
+    assert run_and_check(pkg, what, M, K, N, rank) == ROUTE[route]
+
+
+# the same shapes on every route that can take them (the A/B hook, ltx25_set_lora_route)
+FORCED = [s for s in SHAPES if s[0] in (
+    "x2 upscaler: attn projection", "distilled adapter: rank 450", "video tokens, rank 64",
+    "GEMM pair, ragged M and N", "r first: rank 32 at the FFN width", "r first: rank 16, ragged N")]
+
+
+@pytest.mark.parametrize("forced", [P, RF, F])
+@pytest.mark.parametrize("what,M,K,N,rank,route", FORCED, ids=[s[0] for s in FORCED])
+def test_lora_forced_routes_agree(pkg, dev, what, M, K, N, rank, route, forced):
+    say(f"lora_add forced {forced}: {what}: M={M} K={K} N={N} rank={rank}")
+    pkg.set_lora_route(ROUTE[forced])
+    try:
+        if forced == RF and rank % 8 != 0:
+            # r first needs rank % 8 == 0: refused before any device use, y untouched
+            yd = torch.ones((M, N), dtype=torch.bfloat16, device="cuda")
+            xd = torch.zeros((M, K), dtype=torch.bfloat16, device="cuda")
+            ad = torch.zeros((rank, K), dtype=torch.bfloat16, device="cuda")
+            bd = torch.zeros((N, rank), dtype=torch.bfloat16, device="cuda")
+            with pytest.raises(pkg.Ltx25Error) as e:
+                pkg.lora_add(xd, ad, bd, yd, M, K, N, rank)
+            assert e.value.code == pkg.E_UNSUPPORTED
+            return
+        assert run_and_check(pkg, what, M, K, N, rank) == ROUTE[forced]
+    finally:
+        pkg.set_lora_route(pkg.LORA_AUTO)
 
 
 def test_lora_zero_adapter_leaves_y_bit_identical(pkg, dev):

@@ -342,6 +342,31 @@ def test_i8_epilogue_is_one_fma_then_bf16():
         assert checked >= 50
 
 
+def test_i8_epilogue_with_gelu_is_the_composition():
+    """epilogue 1 = the pinned epilogue's f32 value through the pinned GELU, rounded once;
+    epilogue 0 = orc_i8_epilogue bit for bit."""
+    rng = np.random.default_rng(13)
+    acc = rng.integers(-2_000_000, 2_000_000, (6, 10)).astype(np.int32)
+    sx = (rng.random(6) * 0.03).astype(np.float32)
+    sw = (rng.random(10) * 0.0004).astype(np.float32)
+    bias = rng.standard_normal(10).astype(np.float32)
+    assert np.array_equal(orc.i8_epilogue(acc, sx, sw, bias, 2, epilogue=0),
+                          orc.i8_epilogue(acc, sx, sw, bias, 2))
+    y = orc.i8_epilogue(acc, sx, sw, bias, 2, epilogue=1)
+    checked = 0
+    for m in range(6):
+        for n in range(10):
+            v = _f32_fma_exact(np.float32(acc[m, n]), np.float32(sx[m] * sw[n]), bias[n])
+            if v is None:
+                continue
+            checked += 1
+            g = orc.gelu(np.array([v], np.float32))
+            assert y[m, n] == torch_bf16_bits(g)[0]
+    assert checked >= 50
+    # and GELU changed something: negative pre-activations shrink toward 0
+    assert not np.array_equal(y, orc.i8_epilogue(acc, sx, sw, bias, 2))
+
+
 # ---- low-rank adapter delta ---------------------------------------------------------------
 # The reference's lora test shapes (tests/ltx25-lora-apply-test.cc:394-409), minus the
 # three large ones, which the GPU tests cover.

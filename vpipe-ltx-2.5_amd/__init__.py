@@ -37,6 +37,17 @@ DEQUANT_ONCE_OFF = 0
 DEQUANT_ONCE_ON = 1
 DEQUANT_ONCE_AUTO = 2
 
+TILE_AUTO = 0
+TILE_TALL = 1
+TILE_MID = 2
+TILE_SKINNY = 3
+
+LORA_AUTO = 0
+LORA_NONE = 0
+LORA_PAIR = 1
+LORA_RFIRST = 2
+LORA_FUSED = 3
+
 
 class QWeightC(ctypes.Structure):
     """ltx25_qweight (mirrors QWeight, src/ltx25-metal-ops.h:45-57)."""
@@ -49,6 +60,20 @@ class QWeightC(ctypes.Structure):
         ("bits", ctypes.c_int),
         ("group", ctypes.c_int),
         ("quantized", ctypes.c_int),
+    ]
+
+
+class RouteC(ctypes.Structure):
+    """ltx25_route: what a linear runs on (ltx25_linear_route)."""
+
+    _fields_ = [
+        ("tile", ctypes.c_int),
+        ("i8", ctypes.c_int),
+        ("dequant_once", ctypes.c_int),
+        ("splits", ctypes.c_int),
+        ("slabs", ctypes.c_int),
+        ("slab_rows", ctypes.c_int),
+        ("scratch_bytes", ctypes.c_size_t),
     ]
 
 
@@ -79,6 +104,11 @@ SIGNATURES = {
     "ltx25_dequant_once_takes": (_i, [_i, _i, _i]),
     "ltx25_lora_add": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i]),
     "ltx25_lora_on_matrix_cores": (_i, [_i, _i, _i, _i]),
+    "ltx25_set_lora_matrix_cores": (_i, [_i]),
+    "ltx25_set_lora_route": (_i, [_i]),
+    "ltx25_lora_route": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, ctypes.POINTER(_i)]),
+    "ltx25_set_tile": (_i, [_i]),
+    "ltx25_linear_route": (_i, [_i, _i, _i, _i, ctypes.POINTER(RouteC)]),
     "ltx25_set_i8_gemm": (_i, [_i]),
     "ltx25_i8_takes": (_i, [_i, _i, _i]),
     "ltx25_i8_quantize_rows": (_i, [_vp, _vp, _vp, _vp, _i, _i]),
@@ -241,6 +271,35 @@ def lora_add(x, a, b, y, M: int, K: int, N: int, rank: int, r=None, d=None,
 
 def lora_on_matrix_cores(M: int, K: int, N: int, rank: int) -> bool:
     return bool(load().ltx25_lora_on_matrix_cores(M, K, N, rank))
+
+
+def set_lora_matrix_cores(on: bool) -> None:
+    check(load().ltx25_set_lora_matrix_cores(1 if on else 0))
+
+
+def set_lora_route(route: int) -> None:
+    """LORA_AUTO / LORA_PAIR / LORA_RFIRST / LORA_FUSED for every later lora_add."""
+    check(load().ltx25_set_lora_route(route))
+
+
+def lora_route(x, a, b, y, M: int, K: int, N: int, rank: int) -> int:
+    """The LORA_* route lora_add would take; raises when a forced route cannot."""
+    r = ctypes.c_int(-1)
+    check(load().ltx25_lora_route(_ptr(x), _ptr(a), _ptr(b), _ptr(y), M, K, N, rank,
+                                  ctypes.byref(r)))
+    return r.value
+
+
+def set_tile(tile: int) -> None:
+    """TILE_AUTO / TILE_TALL / TILE_MID / TILE_SKINNY for every later linear."""
+    check(load().ltx25_set_tile(tile))
+
+
+def linear_route(M: int, K: int, N: int, bits: int = 8) -> dict:
+    """The route a linear takes (bits 4 / 8 codes, 16 dense), as a dict."""
+    r = RouteC()
+    check(load().ltx25_linear_route(M, K, N, bits, ctypes.byref(r)))
+    return {f: getattr(r, f) for f, _ in RouteC._fields_}
 
 
 def set_i8_gemm(on: bool) -> None:

@@ -194,7 +194,91 @@ int check_qweight(const ltx25_qweight* w, int K)
 
 int run_i8_linear(DeviceState* ds, hipStream_t st, const void* x,
                   const ltx25_qweight* w, const void* bias, int bias_dtype,
-                  void* y, int M, int K, int N);
+                  void* y, int M, int K, int N, int epilogue);
+
+// Every operand a kernel addresses must stay under 2 GiB: the kernels form
+// 32-bit buffer offsets (voffset + soffset) and a raw buffer's range is a
+// 32-bit byte count. The reference declines the same operands for the same
+// reason -- a wrapped offset computes wrong rows without any error
+// (src/ltx25-metal-ops.cc:342-374). Here the activation and output are cut
+// into row slabs that each stay under the limit; a weight at or over it is
+// refused.
+constexpr size_t kOperandMax = (size_t)1 << 31;
+
+bool below_limit(size_t bytes) { return bytes < kOperandMax; }
+
+size_t weight_bytes(int N, int K, int bits)
+{
+  return (size_t)N * (size_t)K * (size_t)bits / 8;
+}
+
+// Rows per launch so that X [rows][K] and Y [rows][N] (bf16) each stay
+// under kOperandMax: all of M when they do, else a multiple of 256 rows.
+int slab_rows(int M, int K, int N)
+{
+  const size_t widest = (size_t)(K > N ? K : N) * 2;
+  const size_t rows = (kOperandMax - 1) / widest;
+  if ((size_t)M <= rows) { return M; }
+  return (int)(rows & ~(size_t)255);
+}
+
+std::atomic<int> g_tile{LTX25_TILE_AUTO};
+
+// The route a linear takes, decided on the host before any device use.
+struct LinearRoute {
+  bool i8 = false;
+  bool deq_once = false;
+  int rows = 0;      // rows per launch
+  int slabs = 1;
+  ltx25::GemmPlan plan;   // of the first slab
+  size_t scratch = 0;     // bytes of library scratch the call uses
+};
+
+int cu_count_hint()
+{
+  // the CU count of a device already checked, else the MI355X's
+  for (int d = 0; d < kMaxDevices; ++d) {
+    if (g_dev[d].checked && g_dev[d].ok) { return g_dev[d].cu_count; }
+  }
+  return 256;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+size_t i8_scratch_bytes(int M, int K, int N)
+{
+  return align256((size_t)M * K) + align256((size_t)M * 4) + align256((size_t)N * K) +
+         align256((size_t)N * 4);
+}
+
+// bits: 8 or 4 (codes) or 16 (a dense weight).
+int plan_linear(int M, int K, int N, int bits, int cu_count, LinearRoute* r)
+{
+  if (!below_limit(weight_bytes(N, K, bits))) {
+    return fail(LTX25_E_UNSUPPORTED,
+                "the weight [%d][%d] at %d bits is %zu bytes; operands must stay under 2 GiB "
+                "(32-bit buffer offsets)", N, K, bits, weight_bytes(N, K, bits));
+  }
+  r->i8 = ltx25_i8_takes(M, K, N) != 0;
+  if (r->i8) {
+    r->rows = M;
+    r->slabs = 1;
+    r->scratch = i8_scratch_bytes(M, K, N);
+    return LTX25_OK;
+  }
+  r->deq_once = bits != 16 && ltx25_dequant_once_takes(M, K, N) != 0 &&
+                below_limit(weight_bytes(N, K, 16));
+  r->rows = slab_rows(M, K, N);
+  if (r->rows <= 0) {
+    return fail(LTX25_E_UNSUPPORTED, "K=%d N=%d: one row of X or Y is 2 GiB or more", K, N);
+  }
+  r->slabs = (M + r->rows - 1) / r->rows;
+  const int gemm_bits = r->deq_once ? 16 : bits;
+  r->plan = ltx25::plan_gemm(r->rows, N, K, gemm_bits, cu_count,
+                             g_tile.load(std::memory_order_relaxed));
+  r->scratch = r->plan.workspace_bytes + (r->deq_once ? (size_t)N * K * 2 : 0);
+  return LTX25_OK;
+}
 
 int run_linear(hipStream_t st, const void* x, const ltx25_qweight* w,
                const void* bias, int bias_dtype, void* y, int M, int K, int N,
@@ -220,22 +304,22 @@ int run_linear(hipStream_t st, const void* x, const ltx25_qweight* w,
     return fail(LTX25_E_UNSUPPORTED,
                 "K=%d: the MFMA kernels step K by 64; pad K to a multiple of 64", K);
   }
+  const int bits = w->quantized ? w->bits : 16;
+  LinearRoute route;
+  rc = plan_linear(M, K, N, bits, cu_count_hint(), &route);
+  if (rc != LTX25_OK) { return rc; }
   DeviceState* ds = nullptr;
   rc = current_device(&ds);
   if (rc != LTX25_OK) { return rc; }
-
-  if (epilogue == LTX25_EPI_NONE && ltx25_i8_takes(M, K, N)) {
-    return run_i8_linear(ds, st, x, w, bias, bias_dtype, y, M, K, N);
-  }
+  if (route.i8) { return run_i8_linear(ds, st, x, w, bias, bias_dtype, y, M, K, N, epilogue); }
 
   ltx25::GemmDesc d;
-  d.x = (const uint16_t*)x;
   d.w = w->quantized ? w->codes : w->w;
   d.scales = (const uint16_t*)w->scales;
   d.qbias = (const uint16_t*)w->qbias;
-  d.bits = w->quantized ? w->bits : 16;
+  d.bits = bits;
   d.group = w->quantized ? w->group : 64;
-  if (w->quantized && ltx25_dequant_once_takes(M, K, N)) {
+  if (route.deq_once) {
     // The dequant-once arm: expand W into the grow-only bf16 scratch, then
     // the same GEMM tile over the dense copy. The expansion is bit-identical
     // to the in-register dequant, so both arms produce the same bits.
@@ -255,24 +339,26 @@ int run_linear(hipStream_t st, const void* x, const ltx25_qweight* w,
   d.bias = bias;
   d.bias_type = bias != nullptr ? bias_dtype : ltx25::kBiasNone;
   d.epilogue = epilogue;
-  d.y = (uint16_t*)y;
-  d.M = M;
   d.N = N;
   d.K = K;
-  const ltx25::GemmPlan plan = ltx25::plan_gemm(M, N, K, d.bits, ds->cu_count);
-  float* ws = nullptr;
-  if (plan.workspace_bytes > 0) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    rc = grow(&ds->ws, &ds->ws_bytes, plan.workspace_bytes);
-    if (rc != LTX25_OK) { return rc; }
-    ws = (float*)ds->ws;
+  const int tile = g_tile.load(std::memory_order_relaxed);
+  for (int m0 = 0; m0 < M; m0 += route.rows) {
+    d.M = M - m0 < route.rows ? M - m0 : route.rows;
+    d.x = (const uint16_t*)x + (size_t)m0 * K;
+    d.y = (uint16_t*)y + (size_t)m0 * N;
+    const ltx25::GemmPlan plan = ltx25::plan_gemm(d.M, N, K, d.bits, ds->cu_count, tile);
+    float* ws = nullptr;
+    if (plan.workspace_bytes > 0) {
+      std::lock_guard<std::mutex> lk(g_mu);
+      rc = grow(&ds->ws, &ds->ws_bytes, plan.workspace_bytes);
+      if (rc != LTX25_OK) { return rc; }
+      ws = (float*)ds->ws;
+    }
+    const hipError_t e = ltx25::launch_gemm(d, plan, ws, st);
+    if (e != hipSuccess) { return hip_fail(e, "qgemm launch"); }
   }
-  const hipError_t e = ltx25::launch_gemm(d, plan, ws, st);
-  if (e != hipSuccess) { return hip_fail(e, "qgemm launch"); }
   return LTX25_OK;
 }
-
-size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // The int8 tier inside `linear`: quantize the activation per token and the
 // weight per output channel for THIS call (the reference's tier keeps no
@@ -280,8 +366,10 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // int8 GEMM with the fused dequant epilogue.
 int run_i8_linear(DeviceState* ds, hipStream_t st, const void* x,
                   const ltx25_qweight* w, const void* bias, int bias_dtype,
-                  void* y, int M, int K, int N)
+                  void* y, int M, int K, int N, int epilogue)
 {
+  // (plan_linear has checked that M * K, N * K and M * N * 2 stay under
+  // 2 GiB for this tier)
   const size_t xq_b = align256((size_t)M * K);
   const size_t sx_b = align256((size_t)M * 4);
   const size_t wq_b = align256((size_t)N * K);
@@ -307,7 +395,7 @@ int run_i8_linear(DeviceState* ds, hipStream_t st, const void* x,
     e = ltx25::launch_i8_quantize_rows((const uint16_t*)w->w, wq, sw, N, K, st);
   }
   if (e != hipSuccess) { return hip_fail(e, "i8 quantize (w)"); }
-  e = ltx25::launch_i8_gemm(xq, sx, wq, sw, bias, bias != nullptr ? bias_dtype : 0,
+  e = ltx25::launch_i8_gemm(xq, sx, wq, sw, bias, bias != nullptr ? bias_dtype : 0, epilogue,
                             (uint16_t*)y, nullptr, M, K, N, st);
   if (e != hipSuccess) { return hip_fail(e, "i8 gemm launch"); }
   return LTX25_OK;
@@ -325,14 +413,64 @@ constexpr int kLoraPairMinRank = 96;
 // the dense GEMM rather than per column split inside the fused kernel.
 constexpr int kLoraRFirstMinM = 512;
 
-bool lora_pair_takes(int M, int K, int N, int rank, const void* x, const void* y)
+// The LoRA routes' preconditions. Each is what its kernels need to be
+// correct; the AUTO thresholds sit on top of them (lora_route).
+bool lora_pair_ok(int M, int K, int N, int rank, const void* x, const void* y)
 {
-  const size_t two_gib = (size_t)1 << 31;
   const size_t rk = (size_t)((rank + 63) & ~63);
-  return rank >= kLoraPairMinRank && M >= 256 && K % 64 == 0 && N % 8 == 0 &&
-         aligned16(x) && aligned16(y) && (size_t)M * K * 2 < two_gib &&
-         (size_t)M * N * 2 < two_gib && rk * K * 2 < two_gib && (size_t)N * rk * 2 < two_gib &&
-         (size_t)M * rk * 2 < two_gib;
+  return K % 64 == 0 && N % 8 == 0 && aligned16(x) && aligned16(y) &&
+         below_limit((size_t)M * K * 2) && below_limit((size_t)M * N * 2) &&
+         below_limit(rk * K * 2) && below_limit((size_t)N * rk * 2) &&
+         below_limit((size_t)M * rk * 2);
+}
+
+// The fused kernel's vector path: 16-byte operand loads and 32-bit buffer
+// offsets. B is copied with its rank padded to a multiple of 8 when it is
+// not already (so b's alignment is not a condition).
+bool lora_vec_ok(int M, int K, int N, int rank, const void* x, const void* a, const void* y)
+{
+  const int rank8 = (rank + 7) & ~7;
+  return K % 8 == 0 && N % 8 == 0 && aligned16(x) && aligned16(a) && aligned16(y) &&
+         below_limit((size_t)M * K * 2) && below_limit((size_t)M * N * 2) &&
+         below_limit((size_t)rank * K * 2) && below_limit((size_t)N * rank8 * 2);
+}
+
+bool lora_rfirst_ok(int M, int K, int N, int rank, const void* x, const void* a, const void* y)
+{
+  return lora_vec_ok(M, K, N, rank, x, a, y) && K % 64 == 0 && rank % 8 == 0 &&
+         rank <= ltx25::kLoraMaxRank && below_limit((size_t)M * rank * 2);
+}
+
+std::atomic<int> g_lora_force{LTX25_LORA_AUTO};
+
+// The route ltx25_lora_add takes (LTX25_LORA_*), or -1 with the error set
+// when a forced route cannot take the shape.
+int lora_route(int M, int K, int N, int rank, const void* x, const void* a, const void* y)
+{
+  if (M <= 0 || K <= 0 || N <= 0 || rank <= 0) { return LTX25_LORA_NONE; }
+  const int force = g_lora_force.load(std::memory_order_relaxed);
+  if (force == LTX25_LORA_PAIR) {
+    if (lora_pair_ok(M, K, N, rank, x, y)) { return LTX25_LORA_PAIR; }
+    fail(LTX25_E_UNSUPPORTED, "the forced LoRA GEMM pair needs K %% 64 == 0, N %% 8 == 0, "
+         "16-byte aligned x and y and operands under 2 GiB (M=%d K=%d N=%d rank=%d)",
+         M, K, N, rank);
+    return -1;
+  }
+  if (force == LTX25_LORA_RFIRST) {
+    if (lora_rfirst_ok(M, K, N, rank, x, a, y)) { return LTX25_LORA_RFIRST; }
+    fail(LTX25_E_UNSUPPORTED, "the forced r-first LoRA route needs the vector path, "
+         "K %% 64 == 0 and rank %% 8 == 0, rank <= %d (M=%d K=%d N=%d rank=%d)",
+         ltx25::kLoraMaxRank, M, K, N, rank);
+    return -1;
+  }
+  if (force == LTX25_LORA_FUSED) { return LTX25_LORA_FUSED; }
+  if (rank >= kLoraPairMinRank && M >= 256 && lora_pair_ok(M, K, N, rank, x, y)) {
+    return LTX25_LORA_PAIR;
+  }
+  if (M >= kLoraRFirstMinM && lora_rfirst_ok(M, K, N, rank, x, a, y)) {
+    return LTX25_LORA_RFIRST;
+  }
+  return LTX25_LORA_FUSED;
 }
 
 int lora_pair(DeviceState* ds, hipStream_t st, const void* x, const void* a, const void* b,
@@ -535,7 +673,37 @@ int ltx25_dequant_once_takes(int M, int K, int N)
 
 int ltx25_lora_on_matrix_cores(int M, int K, int N, int rank)
 {
-  return M > 0 && K > 0 && N > 0 && rank > 0 ? 1 : 0;
+  // the reference's question: does this shape take the matrix-core GEMM
+  // pair (src/ltx25-metal-ops.cc:921-936)? Pointers as any allocator returns.
+  const void* p = (const void*)(uintptr_t)256;
+  return lora_route(M, K, N, rank, p, p, p) == LTX25_LORA_PAIR ? 1 : 0;
+}
+
+int ltx25_set_lora_matrix_cores(int on)
+{
+  g_lora_force.store(on != 0 ? LTX25_LORA_AUTO : LTX25_LORA_FUSED, std::memory_order_relaxed);
+  return LTX25_OK;
+}
+
+int ltx25_set_lora_route(int route)
+{
+  if (route != LTX25_LORA_AUTO && route != LTX25_LORA_PAIR && route != LTX25_LORA_RFIRST &&
+      route != LTX25_LORA_FUSED) {
+    return fail(LTX25_E_INVAL, "LoRA route %d is not AUTO, PAIR, RFIRST or FUSED", route);
+  }
+  g_lora_force.store(route, std::memory_order_relaxed);
+  return LTX25_OK;
+}
+
+int ltx25_lora_route(const void* x, const void* a, const void* b, const void* y, int M, int K,
+                     int N, int rank, int* route)
+{
+  (void)b;
+  if (route == nullptr) { return fail(LTX25_E_INVAL, "route is null"); }
+  const int r = lora_route(M, K, N, rank, x, a, y);
+  if (r < 0) { return LTX25_E_UNSUPPORTED; }
+  *route = r;
+  return LTX25_OK;
 }
 
 int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
@@ -552,20 +720,16 @@ int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
   if ((((uintptr_t)x | (uintptr_t)a | (uintptr_t)b | (uintptr_t)y) & 1u) != 0) {
     return fail(LTX25_E_INVAL, "a bf16 tensor is not 2-byte aligned");
   }
+  const int route = lora_route(M, K, N, rank, x, a, y);
+  if (route < 0) { return LTX25_E_UNSUPPORTED; }
   DeviceState* ds = nullptr;
   const int rc = current_device(&ds);
   if (rc != LTX25_OK) { return rc; }
-  if (lora_pair_takes(M, K, N, rank, x, y)) {
+  if (route == LTX25_LORA_PAIR) {
     return lora_pair(ds, (hipStream_t)stream, x, a, b, y, M, K, N, rank);
   }
-  // The vector path: 16-byte operand loads and 32-bit buffer offsets. B is
-  // copied with its rank padded to a multiple of 8 when it is not already.
   const int rank8 = (rank + 7) & ~7;
-  const size_t two_gib = (size_t)1 << 31;
-  const bool vec = K % 8 == 0 && N % 8 == 0 && aligned16(x) && aligned16(a) &&
-                   aligned16(y) && (size_t)M * K * 2 < two_gib &&
-                   (size_t)M * N * 2 < two_gib && (size_t)rank * K * 2 < two_gib &&
-                   (size_t)N * rank8 * 2 < two_gib;
+  const bool vec = lora_vec_ok(M, K, N, rank, x, a, y);
   const uint16_t* pa = (const uint16_t*)a;
   const uint16_t* pb = (const uint16_t*)b;
   int ldb = rank;
@@ -581,28 +745,27 @@ int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
     pb = (const uint16_t*)ds->lora_b;
     ldb = rank8;
   }
-  if (vec && M >= kLoraRFirstMinM && K % 64 == 0 && rank % 8 == 0 &&
-      rank <= ltx25::kLoraMaxRank) {
+  if (route == LTX25_LORA_RFIRST) {
     // Many tokens: r = bf16(x . A^T) once with the dense GEMM (A is the
     // [rank][K] weight of that linear), then the fused kernel's second
     // phase reads it -- instead of recomputing x . A^T for every column
     // split of a row block. Same roundings (r rounded once to bf16).
-    uint16_t* r = nullptr;
+    uint16_t* rb = nullptr;
     {
       std::lock_guard<std::mutex> lk(g_mu);
       const int rc2 = grow(&ds->lora_mm, &ds->lora_mm_bytes, (size_t)M * rank * 2);
       if (rc2 != LTX25_OK) { return rc2; }
-      r = (uint16_t*)ds->lora_mm;
+      rb = (uint16_t*)ds->lora_mm;
     }
-    ltx25::GemmDesc d;
-    d.x = (const uint16_t*)x;
-    d.w = pa;
-    d.bits = 16;
-    d.group = 64;
-    d.y = r;
-    d.M = M;
-    d.N = rank;
-    d.K = K;
+    ltx25::GemmDesc gd;
+    gd.x = (const uint16_t*)x;
+    gd.w = pa;
+    gd.bits = 16;
+    gd.group = 64;
+    gd.y = rb;
+    gd.M = M;
+    gd.N = rank;
+    gd.K = K;
     const ltx25::GemmPlan plan = ltx25::plan_gemm(M, rank, K, 16, ds->cu_count);
     float* ws = nullptr;
     if (plan.workspace_bytes > 0) {
@@ -611,10 +774,10 @@ int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
       if (rc2 != LTX25_OK) { return rc2; }
       ws = (float*)ds->ws;
     }
-    hipError_t e = ltx25::launch_gemm(d, plan, ws, (hipStream_t)stream);
+    hipError_t e = ltx25::launch_gemm(gd, plan, ws, (hipStream_t)stream);
     if (e != hipSuccess) { return hip_fail(e, "lora r gemm launch"); }
     e = ltx25::launch_lora((const uint16_t*)x, pa, pb, (uint16_t*)y, M, K, N, rank, ldb, vec,
-                           ds->cu_count, (hipStream_t)stream, r);
+                           ds->cu_count, (hipStream_t)stream, rb);
     if (e != hipSuccess) { return hip_fail(e, "lora launch"); }
     return LTX25_OK;
   }
@@ -637,9 +800,48 @@ int ltx25_set_i8_gemm(int on)
 int ltx25_i8_takes(int M, int K, int N)
 {
   return g_i8_on.load(std::memory_order_relaxed) != 0 && M >= 1024 && K >= 1024 &&
-                 K % 128 == 0 && N >= 16
+                 K % 128 == 0 && N >= 16 && below_limit((size_t)M * K) &&
+                 below_limit((size_t)N * K) && below_limit((size_t)M * N * 2)
              ? 1
              : 0;
+}
+
+int ltx25_set_tile(int tile)
+{
+  if (tile != LTX25_TILE_AUTO && tile != LTX25_TILE_TALL && tile != LTX25_TILE_MID &&
+      tile != LTX25_TILE_SKINNY) {
+    return fail(LTX25_E_INVAL, "tile %d is not AUTO, TALL, MID or SKINNY", tile);
+  }
+  g_tile.store(tile, std::memory_order_relaxed);
+  return LTX25_OK;
+}
+
+int ltx25_linear_route(int M, int K, int N, int bits, ltx25_route* out)
+{
+  if (out == nullptr) { return fail(LTX25_E_INVAL, "out is null"); }
+  int rc = check_shape(M, K, N);
+  if (rc != LTX25_OK) { return rc; }
+  if (bits != 4 && bits != 8 && bits != 16) {
+    return fail(LTX25_E_INVAL, "bits=%d; 4 or 8 (codes) or 16 (dense)", bits);
+  }
+  if (K % 64 != 0) {
+    return fail(LTX25_E_UNSUPPORTED,
+                "K=%d: the MFMA kernels step K by 64; pad K to a multiple of 64", K);
+  }
+  LinearRoute r;
+  rc = plan_linear(M, K, N, bits, cu_count_hint(), &r);
+  if (rc != LTX25_OK) { return rc; }
+  std::memset(out, 0, sizeof *out);
+  out->i8 = r.i8 ? 1 : 0;
+  out->dequant_once = r.deq_once ? 1 : 0;
+  out->tile = r.i8 ? 0
+                   : (r.plan.tile == 0 ? LTX25_TILE_TALL
+                                       : r.plan.tile == 1 ? LTX25_TILE_MID : LTX25_TILE_SKINNY);
+  out->splits = r.i8 ? 1 : r.plan.splits;
+  out->slabs = r.slabs;
+  out->slab_rows = r.rows;
+  out->scratch_bytes = r.scratch;
+  return LTX25_OK;
 }
 
 int ltx25_i8_quantize_rows(void* stream, const void* x_bf16, int8_t* q,
@@ -713,7 +915,7 @@ int ltx25_i8_gemm(void* stream, const int8_t* xq, const float* sx,
   if (rc != LTX25_OK) { return rc; }
   const hipError_t e = ltx25::launch_i8_gemm(xq, sx, wq, sw, bias,
                                              bias != nullptr ? bias_dtype : 0,
-                                             (uint16_t*)y, acc_dbg, M, K, N,
+                                             ltx25::kEpiNone, (uint16_t*)y, acc_dbg, M, K, N,
                                              (hipStream_t)stream);
   return e == hipSuccess ? LTX25_OK : hip_fail(e, "i8 gemm launch");
 }

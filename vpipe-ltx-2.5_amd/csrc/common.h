@@ -14,6 +14,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int v2i32 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
@@ -113,10 +114,14 @@ struct GemmPlan {
   int splits = 1;    // split-K factor
   int k_chunk = 0;   // K elements per split (multiple of 64)
   size_t workspace_bytes = 0;   // f32 partials when splits > 1
+  int cu_count = 256;           // CUs of the device planned for (persistent grids)
 };
 
 // `bits` is the weight format the GEMM reads: 8 or 4 (codes) or 16 (dense).
-GemmPlan plan_gemm(int M, int N, int K, int bits, int cu_count);
+// `force` (the LTX25_TILE_* values): 0 the planner's choice; 1 the
+// 256 x 256 tile; 2 the 128 x 128 split-K tile; 3 the M <= 128 kernel
+// where it takes the shape, else the planner's choice.
+GemmPlan plan_gemm(int M, int N, int K, int bits, int cu_count, int force = 0);
 hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
                        float* workspace, hipStream_t stream);
 // The M <= 128 route (skinny.hip): 32 output columns per workgroup, K split
@@ -179,9 +184,11 @@ hipError_t launch_i8_quantize_qweight(const void* codes,
                                       const uint16_t* qbias, int bits,
                                       int group, int8_t* q, float* s, int N,
                                       int K, hipStream_t stream);
+// y = bf16(epilogue(fma(float(acc), sx[m] * sw[n], bias[n]))), epilogue
+// kEpiNone or kEpiGelu (GELU-tanh in f32 before the one rounding).
 hipError_t launch_i8_gemm(const int8_t* xq, const float* sx,
                           const int8_t* wq, const float* sw, const void* bias,
-                          int bias_type, uint16_t* y, int32_t* acc, int M,
-                          int K, int N, hipStream_t stream);
+                          int bias_type, int epilogue, uint16_t* y, int32_t* acc,
+                          int M, int K, int N, hipStream_t stream);
 
 }  // namespace ltx25

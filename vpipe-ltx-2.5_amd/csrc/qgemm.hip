@@ -603,7 +603,7 @@ qgemm_kernel(KParams p)
               v[t] = acc[i][j][4 * g + t] + bv[g][t];
             }
           }
-          if (!I8 && p.epilogue == kEpiGelu) {
+          if (p.epilogue == kEpiGelu) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) { v[t] = gelu_tanh(v[t]); }
           }
@@ -731,12 +731,15 @@ int ilog2(int v)
 
 }  // namespace
 
-GemmPlan plan_gemm(int M, int N, int K, int bits, int cu_count)
+GemmPlan plan_gemm(int M, int N, int K, int bits, int cu_count, int force)
 {
   GemmPlan plan;
-  if (plan_skinny(M, N, K, bits, cu_count, plan)) { return plan; }
+  plan.cu_count = cu_count;
+  if ((force == 0 || force == 3) && plan_skinny(M, N, K, bits, cu_count, plan)) { return plan; }
   const long tall_tiles = (long)((M + 255) / 256) * ((N + 255) / 256);
-  if (M > 128 && tall_tiles >= cu_count) {
+  // a forced M <= 128 kernel that cannot take the shape leaves the choice
+  // to the planner
+  if (force == 1 || ((force == 0 || force == 3) && M > 128 && tall_tiles >= cu_count)) {
     plan.tile = 0;
     plan.splits = 1;
     plan.k_chunk = K;
@@ -761,8 +764,8 @@ GemmPlan plan_gemm(int M, int N, int K, int bits, int cu_count)
 }
 
 hipError_t launch_i8_gemm(const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
-                          const void* bias, int bias_type, uint16_t* y, int32_t* acc, int M,
-                          int K, int N, hipStream_t stream)
+                          const void* bias, int bias_type, int epilogue, uint16_t* y, int32_t* acc,
+                          int M, int K, int N, hipStream_t stream)
 {
   KParams kp = {};
   kp.xq = xq;
@@ -772,7 +775,7 @@ hipError_t launch_i8_gemm(const int8_t* xq, const float* sx, const int8_t* wq, c
   kp.wq = (const uint8_t*)wq;
   kp.bias = bias;
   kp.bias_type = bias != nullptr ? bias_type : kBiasNone;
-  kp.epilogue = kEpiNone;
+  kp.epilogue = epilogue;
   kp.y = y;
   kp.M = M;
   kp.N = N;
