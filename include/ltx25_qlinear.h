@@ -112,6 +112,29 @@ int ltx25_linear_q_ex(void* stream, const void* x, const ltx25_qweight* w,
                       const void* bias, int bias_dtype, void* y, int M, int K,
                       int N, int epilogue);
 
+/* ltx25_linear_q_ex that allocates nothing: no hipMalloc, hipFree or
+ * allocating library call, on any call. No counterpart in the reference;
+ * it is for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation). Same kernels and
+ * the same output bits as ltx25_linear_q_ex with the int8 tier off (the
+ * in-register dequant stands in for the dequant-once expansion, which
+ * produces the same bits). Split-K partials go to a fixed device array of
+ * ltx25_noalloc_scratch_bytes() per GPU, held until the process ends and
+ * resolved per device by ltx25_init or on the first call there (the HIP
+ * runtime places the array in device memory at that point: call
+ * ltx25_init on each device before capture or the serving loop).
+ * LTX25_E_UNSUPPORTED when the plan's partials exceed that size, or when
+ * the int8 tier is on and takes the shape. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (two streams, two
+ * threads) race; calls ordered on one stream do not. Nothing in the array
+ * needs to start at zero: each split writes its whole partial. */
+int ltx25_linear_q_noalloc(void* stream, const void* x, const ltx25_qweight* w,
+                           const void* bias, int bias_dtype, void* y, int M, int K,
+                           int N, int epilogue);
+
+/* Bytes of the no-allocation linear's per-GPU scratch (32 MiB). */
+size_t ltx25_noalloc_scratch_bytes(void);
+
 /* Dense bf16 linear: y = x . w^T (+ bias). K must be a multiple of 64.
  * Replaces the dense MetalOps::linear (src/ltx25-metal-ops.h:82-87;
  * src/ltx25-metal-ops.cc:504-529). */

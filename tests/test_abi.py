@@ -19,7 +19,7 @@ def declared_entry_points():
     for f in os.listdir(INCLUDE):
         if f.endswith(".h"):
             text = open(os.path.join(INCLUDE, f)).read()
-            names |= set(re.findall(r"^\s*(?:int|const char\*|void)\s+(ltx25_\w+)\s*\(", text,
+            names |= set(re.findall(r"^\s*(?:int|const char\*|void|size_t)\s+(ltx25_\w+)\s*\(", text,
                                     re.M))
     return sorted(names)
 
@@ -265,3 +265,43 @@ def test_operand_limit_slabs_and_refusal(pkg, lib):
         assert r(8160, 4096, 16384)["i8"] == 1
     finally:
         pkg.set_i8_gemm(False)
+
+
+def test_noalloc_refuses_the_int8_tier_before_device_use(pkg, lib):
+    """The no-allocation linear cannot quantize into library scratch: with
+    the tier on and taking the shape it fails before any HIP call."""
+    import ctypes
+
+    fake = 0x10000
+    q = pkg.QWeightC(None, fake, fake, fake, 8, 64, 1)
+    pkg.set_i8_gemm(True)
+    try:
+        assert pkg.i8_takes(1024, 2048, 2048)
+        rc = lib.ltx25_linear_q_noalloc(None, fake, ctypes.byref(q), None, 0, fake, 1024, 2048,
+                                        2048, 0)
+        assert rc == pkg.E_UNSUPPORTED
+        assert "int8" in pkg.last_error()
+    finally:
+        pkg.set_i8_gemm(False)
+    # malformed calls fail validation exactly as linear_q_ex does
+    assert lib.ltx25_linear_q_noalloc(None, fake, ctypes.byref(q), None, 0, fake, 16, 100, 128,
+                                      0) == pkg.E_INVAL
+
+
+def test_every_planned_split_fits_the_noalloc_scratch(pkg):
+    """Split-K partials of every plan the planner makes for a 256-CU device
+    fit the no-allocation linear's 32 MiB: the M <= 128 kernel keeps
+    (N / 32) x splits within 3 workgroups per CU, and the 128 x 128 tile
+    splits only until its workgroups cover the CUs once."""
+    cap = pkg.noalloc_scratch_bytes()
+    worst = 0
+    for M in [1, 16, 64, 126, 128, 129, 192, 255, 256, 300, 384, 512, 640, 1000, 1024, 2040,
+              4080]:
+        for N in [64, 260, 1000, 2048, 4096, 6144, 8192, 16384, 32640]:
+            for K in [64, 512, 2048, 4096, 8192, 16384, 65536]:
+                if N * K * 2 >= 2 ** 31:
+                    continue        # a weight the linear refuses
+                r = pkg.linear_route(M, K, N, bits=16)
+                worst = max(worst, r["scratch_bytes"])
+                assert r["scratch_bytes"] <= cap, (M, K, N, r)
+    assert worst > cap // 4        # the scan reaches plans near the cap

@@ -95,6 +95,9 @@ SIGNATURES = {
     "ltx25_quant_available": (_i, []),
     "ltx25_linear_q": (_i, [_vp, _vp, ctypes.POINTER(QWeightC), _vp, _i, _vp, _i, _i, _i]),
     "ltx25_linear_q_ex": (_i, [_vp, _vp, ctypes.POINTER(QWeightC), _vp, _i, _vp, _i, _i, _i, _i]),
+    "ltx25_linear_q_noalloc": (_i, [_vp, _vp, ctypes.POINTER(QWeightC), _vp, _i, _vp, _i, _i, _i,
+                                    _i]),
+    "ltx25_noalloc_scratch_bytes": (_sz, []),
     "ltx25_linear": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i]),
     "ltx25_bias_add": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "ltx25_gelu_tanh": (_i, [_vp, _vp, _vp, _sz]),
@@ -210,6 +213,19 @@ def linear_q(x, w: QWeight, bias, y, M: int, K: int, N: int, epilogue: int = EPI
     cw = w.c()
     check(load().ltx25_linear_q_ex(_stream(stream), _ptr(x), ctypes.byref(cw), _ptr(bias),
                                    bias_dtype_of(bias), _ptr(y), M, K, N, epilogue))
+
+
+def linear_q_noalloc(x, w: QWeight, bias, y, M: int, K: int, N: int, epilogue: int = EPI_NONE,
+                     stream=None) -> None:
+    """linear_q that allocates nothing: split-K partials in the library's fixed
+    per-GPU scratch (noalloc_scratch_bytes()); overlapping calls on one GPU race."""
+    cw = w.c()
+    check(load().ltx25_linear_q_noalloc(_stream(stream), _ptr(x), ctypes.byref(cw), _ptr(bias),
+                                        bias_dtype_of(bias), _ptr(y), M, K, N, epilogue))
+
+
+def noalloc_scratch_bytes() -> int:
+    return int(load().ltx25_noalloc_scratch_bytes())
 
 
 def linear(x, w, bias, y, M: int, K: int, N: int, stream=None) -> None:

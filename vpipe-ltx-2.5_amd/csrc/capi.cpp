@@ -12,6 +12,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -280,9 +281,13 @@ int plan_linear(int M, int K, int N, int bits, int cu_count, LinearRoute* r)
   return LTX25_OK;
 }
 
+// `noalloc`: the ltx25_linear_q_noalloc variant. It plans the same GEMM
+// without the routes that need library scratch (the int8 tier, the
+// dequant-once expansion) and puts split-K partials in the fixed device
+// array of noalloc.hip, refusing a plan whose partials do not fit.
 int run_linear(hipStream_t st, const void* x, const ltx25_qweight* w,
                const void* bias, int bias_dtype, void* y, int M, int K, int N,
-               int epilogue)
+               int epilogue, bool noalloc = false)
 {
   if (x == nullptr || y == nullptr) { return fail(LTX25_E_INVAL, "x or y is null"); }
   int rc = check_shape(M, K, N);
@@ -308,10 +313,41 @@ int run_linear(hipStream_t st, const void* x, const ltx25_qweight* w,
   LinearRoute route;
   rc = plan_linear(M, K, N, bits, cu_count_hint(), &route);
   if (rc != LTX25_OK) { return rc; }
+  if (noalloc) {
+    if (route.i8) {
+      return fail(LTX25_E_UNSUPPORTED,
+                  "the int8 tier takes M=%d K=%d N=%d and quantizes into library scratch; "
+                  "the no-allocation linear cannot run it (ltx25_set_i8_gemm(0) turns it off)",
+                  M, K, N);
+    }
+    // the in-register dequant: bit-identical to the dequant-once arm
+    route.deq_once = false;
+  }
   DeviceState* ds = nullptr;
   rc = current_device(&ds);
   if (rc != LTX25_OK) { return rc; }
   if (route.i8) { return run_i8_linear(ds, st, x, w, bias, bias_dtype, y, M, K, N, epilogue); }
+  const int tile = g_tile.load(std::memory_order_relaxed);
+  float* fixed_ws = nullptr;
+  if (noalloc) {
+    // every slab's plan must fit the fixed scratch before anything launches
+    // (the slabs are `rows` tall except a shorter last one)
+    const int last = M - (route.slabs - 1) * route.rows;
+    const size_t need =
+        std::max(ltx25::plan_gemm(route.rows, N, K, bits, ds->cu_count, tile).workspace_bytes,
+                 ltx25::plan_gemm(last, N, K, bits, ds->cu_count, tile).workspace_bytes);
+    if (need > ltx25::kNoAllocScratchBytes) {
+      return fail(LTX25_E_UNSUPPORTED,
+                  "M=%d K=%d N=%d: the split-K partials need %zu bytes; the no-allocation "
+                  "linear's scratch holds %zu", M, K, N, need, ltx25::kNoAllocScratchBytes);
+    }
+    if (need > 0) {
+      void* p = nullptr;
+      const hipError_t e = ltx25::noalloc_scratch(&p);
+      if (e != hipSuccess) { return hip_fail(e, "hipGetSymbolAddress (no-allocation scratch)"); }
+      fixed_ws = (float*)p;
+    }
+  }
 
   ltx25::GemmDesc d;
   d.w = w->quantized ? w->codes : w->w;
@@ -341,14 +377,15 @@ int run_linear(hipStream_t st, const void* x, const ltx25_qweight* w,
   d.epilogue = epilogue;
   d.N = N;
   d.K = K;
-  const int tile = g_tile.load(std::memory_order_relaxed);
   for (int m0 = 0; m0 < M; m0 += route.rows) {
     d.M = M - m0 < route.rows ? M - m0 : route.rows;
     d.x = (const uint16_t*)x + (size_t)m0 * K;
     d.y = (uint16_t*)y + (size_t)m0 * N;
     const ltx25::GemmPlan plan = ltx25::plan_gemm(d.M, N, K, d.bits, ds->cu_count, tile);
     float* ws = nullptr;
-    if (plan.workspace_bytes > 0) {
+    if (noalloc) {
+      ws = fixed_ws;
+    } else if (plan.workspace_bytes > 0) {
       std::lock_guard<std::mutex> lk(g_mu);
       rc = grow(&ds->ws, &ds->ws_bytes, plan.workspace_bytes);
       if (rc != LTX25_OK) { return rc; }
@@ -544,7 +581,13 @@ extern "C" {
 int ltx25_init(void)
 {
   DeviceState* ds = nullptr;
-  return current_device(&ds);
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  // set-up of the no-allocation linear: this device's scratch address
+  void* p = nullptr;
+  const hipError_t e = ltx25::noalloc_scratch(&p);
+  if (e != hipSuccess) { return hip_fail(e, "hipGetSymbolAddress (no-allocation scratch)"); }
+  return LTX25_OK;
 }
 
 const char* ltx25_last_error(void) { return g_err.c_str(); }
@@ -570,6 +613,15 @@ int ltx25_linear_q_ex(void* stream, const void* x, const ltx25_qweight* w,
   return run_linear((hipStream_t)stream, x, w, bias, bias_dtype, y, M, K, N,
                     epilogue);
 }
+
+int ltx25_linear_q_noalloc(void* stream, const void* x, const ltx25_qweight* w,
+                           const void* bias, int bias_dtype, void* y, int M, int K, int N,
+                           int epilogue)
+{
+  return run_linear((hipStream_t)stream, x, w, bias, bias_dtype, y, M, K, N, epilogue, true);
+}
+
+size_t ltx25_noalloc_scratch_bytes(void) { return ltx25::kNoAllocScratchBytes; }
 
 int ltx25_linear(void* stream, const void* x, const void* w_bf16,
                  const void* bias, int bias_dtype, void* y, int M, int K,

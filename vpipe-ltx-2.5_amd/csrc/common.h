@@ -130,6 +130,11 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
 bool plan_skinny(int M, int N, int K, int bits, int cu_count, GemmPlan& plan);
 hipError_t launch_skinny(const GemmDesc& d, const GemmPlan& plan, float* workspace,
                          hipStream_t stream);
+// The no-allocation linear's split-K scratch (noalloc.hip): a fixed device
+// array of kNoAllocScratchBytes per GPU. noalloc_scratch() returns the
+// current device's copy, resolving its address on the first call there.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+hipError_t noalloc_scratch(void** out);
 // Sums `splits` f32 partial planes [M][N] in split order, adds bias and
 // y_in, applies the epilogue and rounds to bf16 once.
 hipError_t launch_splitk_reduce(const float* partial, int splits, const void* bias, int bias_type,
