@@ -367,6 +367,35 @@ def bench_lora(pkg, torch, steps, warmup):
         out[f"rank{rank}"] = {"us": ms * 1e3, "GBps": byt / (ms * 1e-3) / 1e9,
                               "TFLOPs": flop / (ms * 1e-3) / 1e12,
                               "frac_of_linear": None}
+    # The adapter on the linear it rides on (the FFN up-projection with GELU, rank 32):
+    # the linear alone, the linear with the adapter folded into its GEMM
+    # (ltx25_linear_q_lora), and the reference's sequence (linear, lora_add, GELU),
+    # interleaved best-of-N.
+    w = make_qweight(pkg, torch, N, K, g)
+    h = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    rank = 32
+    a = (torch.randn((rank, K), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    b = (torch.randn((N, rank), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+
+    def seq():
+        pkg.linear_q(x, w, None, h, M, K, N)
+        pkg.lora_add(x, a, b, h, M, K, N, rank)
+        pkg.gelu_tanh(h, h)
+    ab = interleaved(torch, {
+        "linear": lambda: pkg.linear_q(x, w, None, h, M, K, N, pkg.EPI_GELU_TANH),
+        "fold": lambda: pkg.linear_q_lora(x, w, None, a, b, rank, h, M, K, N,
+                                          pkg.EPI_GELU_TANH),
+        "sequence": seq,
+    }, rounds=max(10, steps))
+    lin = ab["linear"]["best_ms"]
+    out["rank32_with_linear"] = {
+        "fold_taken": pkg.lora_fold_takes(M, K, N, rank, 8),
+        "linear_us": lin * 1e3,
+        "fold_us": ab["fold"]["best_ms"] * 1e3,
+        "sequence_us": ab["sequence"]["best_ms"] * 1e3,
+        "fold_overhead_frac": ab["fold"]["best_ms"] / lin - 1.0,
+        "sequence_overhead_frac": ab["sequence"]["best_ms"] / lin - 1.0,
+    }
     return out
 
 
@@ -814,7 +843,8 @@ def main():
         extra["lora"] = bench_lora(pkg, torch, max(5, args.steps // 2), args.warmup)
         ffn_ms = ffn["up_ms"]
         for v in extra["lora"].values():
-            v["frac_of_linear"] = v["us"] * 1e-3 / ffn_ms
+            if "us" in v:
+                v["frac_of_linear"] = v["us"] * 1e-3 / ffn_ms
         extra["ab_interleaved"] = bench_dequant_once(pkg, torch, max(5, args.steps // 2),
                                                      args.warmup)
         log(f"  {extra['lora']}\n  {extra['ab_interleaved']}")

@@ -294,6 +294,29 @@ int ltx25_set_lora_route(int route);
 int ltx25_lora_route(const void* x, const void* a, const void* b, const void* y, int M, int K,
                      int N, int rank, int* route);
 
+/* A quantized linear with its adapter, in the reference's order --
+ *   y = epilogue(x . dequant(W)^T + bias + bf16(x . A^T) . B^T),
+ * the adapter added BEFORE the epilogue's GELU -- as one call.
+ * Replaces the pair a block's call sites issue: MetalOps::linear(QWeight)
+ * then MetalBlock::lora_ -> MetalOps::lora_add on the same output
+ * (src/ltx25-block-metal.cc:428-436,523-524,639-648; ff_in's GELU after
+ * both, :645). Where ltx25_lora_fold_takes says so (the dequant-once arm
+ * of a quantized weight: M >= LTX25_DEQUANT_ONCE_AUTO_MIN_M under AUTO)
+ * the adapter is folded into the linear's GEMM as rank-rounded-to-64 more
+ * K: y = epi([x | r] . [W | B]^T + bias), r = bf16(x . A^T), one rounding
+ * to bf16 where the reference rounds the linear and the delta separately.
+ * Elsewhere it runs ltx25_linear_q, ltx25_lora_add, then ltx25_gelu_tanh
+ * for LTX25_EPI_GELU_TANH. a is bf16 [rank][K], b bf16 [N][rank];
+ * rank 0 is a plain linear. */
+int ltx25_linear_q_lora(void* stream, const void* x, const ltx25_qweight* w, const void* bias,
+                        int bias_dtype, const void* a, const void* b, int rank, void* y, int M,
+                        int K, int N, int epilogue);
+
+/* 1 when ltx25_linear_q_lora folds the adapter into the linear's GEMM for
+ * this shape (bits 4 or 8: the weight's code width) under the current
+ * switches, with allocator-aligned x and y, else 0. Host-only. */
+int ltx25_lora_fold_takes(int M, int K, int N, int rank, int bits);
+
 /* ---- the int8 tier ------------------------------------------------------------ */
 
 /* Turn the int8 tier on (1) or off (0) for ltx25_linear / ltx25_linear_q.

@@ -110,6 +110,9 @@ SIGNATURES = {
     "ltx25_set_lora_matrix_cores": (_i, [_i]),
     "ltx25_set_lora_route": (_i, [_i]),
     "ltx25_lora_route": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, ctypes.POINTER(_i)]),
+    "ltx25_linear_q_lora": (_i, [_vp, _vp, ctypes.POINTER(QWeightC), _vp, _i, _vp, _vp, _i, _vp,
+                                 _i, _i, _i, _i]),
+    "ltx25_lora_fold_takes": (_i, [_i, _i, _i, _i, _i]),
     "ltx25_set_tile": (_i, [_i]),
     "ltx25_linear_route": (_i, [_i, _i, _i, _i, ctypes.POINTER(RouteC)]),
     "ltx25_set_i8_gemm": (_i, [_i]),
@@ -226,6 +229,21 @@ def linear_q_noalloc(x, w: QWeight, bias, y, M: int, K: int, N: int, epilogue: i
 
 def noalloc_scratch_bytes() -> int:
     return int(load().ltx25_noalloc_scratch_bytes())
+
+
+def linear_q_lora(x, w: QWeight, bias, a, b, rank: int, y, M: int, K: int, N: int,
+                  epilogue: int = EPI_NONE, stream=None) -> None:
+    """The linear and its adapter (a [rank][K], b [N][rank]) in one call, the
+    adapter added before the epilogue; folded into the GEMM where
+    lora_fold_takes says so."""
+    cw = w.c()
+    check(load().ltx25_linear_q_lora(_stream(stream), _ptr(x), ctypes.byref(cw), _ptr(bias),
+                                     bias_dtype_of(bias), _ptr(a), _ptr(b), rank, _ptr(y), M, K,
+                                     N, epilogue))
+
+
+def lora_fold_takes(M: int, K: int, N: int, rank: int, bits: int = 8) -> bool:
+    return bool(load().ltx25_lora_fold_takes(M, K, N, rank, bits))
 
 
 def linear(x, w, bias, y, M: int, K: int, N: int, stream=None) -> None:

@@ -574,6 +574,132 @@ int lora_pair(DeviceState* ds, hipStream_t st, const void* x, const void* a, con
   return LTX25_OK;
 }
 
+// The LoRA fold: the adapter rides inside the linear's own GEMM as extra K,
+//   y = epi([x | r] . [W | B]^T + bias),  r = bf16(x . A^T),
+// where W is the dequant-once expansion written with row stride K + rk
+// (rk = rank rounded up to 64) and B fills the last rk columns of each row
+// (zeros past `rank`), and r [M][rk] comes from the dense GEMM over A
+// padded to rk zero rows. The delta costs the r GEMM and rk / K more of
+// the linear, instead of a second pass over y (read + write). Rounding:
+// one bf16 rounding of x . W^T + bias + r . B^T, where the reference's
+// linear + lora_add round twice (src/ltx25-metal-ops.cc:940-1004); before
+// the GELU, as the reference applies the adapter
+// (src/ltx25-block-metal.cc:639-648).
+struct FoldPlan {
+  bool takes = false;
+  int rk = 0;
+  int bits = 0;
+  ltx25::GemmPlan r_plan;
+  ltx25::GemmPlan plan;
+};
+
+FoldPlan plan_fold(int M, int K, int N, int rank, int bits, int cu_count, const void* x,
+                   const void* y)
+{
+  FoldPlan f;
+  if (M <= 0 || K <= 0 || N <= 0 || rank <= 0 || (bits != 8 && bits != 4)) { return f; }
+  if (K % 64 != 0 || N % 8 != 0 || (x != nullptr && !aligned16(x)) ||
+      (y != nullptr && !aligned16(y))) {
+    return f;
+  }
+  LinearRoute route;
+  if (plan_linear(M, K, N, bits, cu_count, &route) != LTX25_OK) {
+    g_err.clear();
+    return f;
+  }
+  if (route.i8 || !route.deq_once || route.slabs != 1) { return f; }
+  const int rk = (rank + 63) & ~63;
+  const int kt = K + rk;
+  if (!below_limit((size_t)N * kt * 2) || !below_limit((size_t)M * rk * 2) ||
+      !below_limit((size_t)rk * K * 2) || !below_limit((size_t)M * K * 2) ||
+      !below_limit((size_t)M * N * 2)) {
+    return f;
+  }
+  const int tile = g_tile.load(std::memory_order_relaxed);
+  f.plan = ltx25::plan_gemm(M, N, kt, 16, cu_count, tile);
+  if (f.plan.tile == 2) { return f; }
+  f.r_plan = ltx25::plan_gemm(M, rk, K, 16, cu_count);
+  f.rk = rk;
+  f.bits = bits;
+  f.takes = true;
+  return f;
+}
+
+int run_fold(DeviceState* ds, hipStream_t st, const FoldPlan& f, const void* x,
+             const ltx25_qweight* w, const void* bias, int bias_dtype, const void* a,
+             const void* b, int rank, void* y, int M, int K, int N, int epilogue)
+{
+  const int rk = f.rk;
+  const int kt = K + rk;
+  // A [rank][K] is read as an [rk][K] weight whose rows past `rank` are
+  // zeros (the buffer range stops at A's end); copied with zero rows only
+  // when it is not 16-byte aligned or the r GEMM plans the M <= 128 kernel
+  const bool pad_a = !aligned16(a) || f.r_plan.tile == 2;
+  const size_t a_bytes = pad_a ? align256((size_t)rk * K * 2) : 0;
+  const size_t r_bytes = align256((size_t)M * rk * 2);
+  uint16_t* wd = nullptr;
+  char* base = nullptr;
+  float* ws = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int rc = grow(&ds->deq, &ds->deq_bytes, (size_t)N * kt * 2);
+    if (rc != LTX25_OK) { return rc; }
+    rc = grow(&ds->lora_mm, &ds->lora_mm_bytes, a_bytes + r_bytes);
+    if (rc != LTX25_OK) { return rc; }
+    const size_t wsb = std::max(f.plan.workspace_bytes, f.r_plan.workspace_bytes);
+    if (wsb > 0) {
+      rc = grow(&ds->ws, &ds->ws_bytes, wsb);
+      if (rc != LTX25_OK) { return rc; }
+      ws = (float*)ds->ws;
+    }
+    wd = (uint16_t*)ds->deq;
+    base = (char*)ds->lora_mm;
+  }
+  // [W | B]: the expansion at row stride K + rk, B in each row's last rk columns
+  hipError_t e = ltx25::launch_dequant(w->codes, (const uint16_t*)w->scales,
+                                       (const uint16_t*)w->qbias, w->bits, w->group, wd, N, K,
+                                       st, kt, (const uint16_t*)b, rank, rank);
+  if (e != hipSuccess) { return hip_fail(e, "fold: dequant launch"); }
+  // r = bf16(x . A^T) over A padded to rk rows
+  const uint16_t* pa = (const uint16_t*)a;
+  if (pad_a) {
+    e = ltx25::launch_lora_pad(pa, 1, rank * K, rank * K, (uint16_t*)base, rk * K, st);
+    if (e != hipSuccess) { return hip_fail(e, "fold: A pad launch"); }
+    pa = (const uint16_t*)base;
+  }
+  uint16_t* r = (uint16_t*)(base + a_bytes);
+  ltx25::GemmDesc rd;
+  rd.x = (const uint16_t*)x;
+  rd.w = pa;
+  rd.bits = 16;
+  rd.group = 64;
+  rd.y = r;
+  rd.M = M;
+  rd.N = rk;
+  rd.wn = pad_a ? rk : rank;
+  rd.K = K;
+  e = ltx25::launch_gemm(rd, f.r_plan, ws, st);
+  if (e != hipSuccess) { return hip_fail(e, "fold: r gemm launch"); }
+  // y = epi([x | r] . [W | B]^T + bias)
+  ltx25::GemmDesc d;
+  d.x = (const uint16_t*)x;
+  d.x2 = r;
+  d.kx = K;
+  d.w = wd;
+  d.bits = 16;
+  d.group = 64;
+  d.bias = bias;
+  d.bias_type = bias != nullptr ? bias_dtype : ltx25::kBiasNone;
+  d.epilogue = epilogue;
+  d.y = (uint16_t*)y;
+  d.M = M;
+  d.N = N;
+  d.K = kt;
+  e = ltx25::launch_gemm(d, f.plan, ws, st);
+  if (e != hipSuccess) { return hip_fail(e, "fold: gemm launch"); }
+  return LTX25_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -840,6 +966,61 @@ int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
                                             ds->cu_count, (hipStream_t)stream);
     if (e != hipSuccess) { return hip_fail(e, "lora launch"); }
   }
+  return LTX25_OK;
+}
+
+int ltx25_lora_fold_takes(int M, int K, int N, int rank, int bits)
+{
+  return plan_fold(M, K, N, rank, bits, cu_count_hint(), nullptr, nullptr).takes ? 1 : 0;
+}
+
+int ltx25_linear_q_lora(void* stream, const void* x, const ltx25_qweight* w, const void* bias,
+                        int bias_dtype, const void* a, const void* b, int rank, void* y, int M,
+                        int K, int N, int epilogue)
+{
+  hipStream_t st = (hipStream_t)stream;
+  if (rank > 0 && (a == nullptr || b == nullptr)) { return fail(LTX25_E_INVAL, "a or b is null"); }
+  if (rank < 0) { return fail(LTX25_E_INVAL, "rank %d is negative", rank); }
+  if (rank == 0 || M <= 0 || K <= 0 || N <= 0) {
+    return run_linear(st, x, w, bias, bias_dtype, y, M, K, N, epilogue);
+  }
+  if ((((uintptr_t)a | (uintptr_t)b) & 1u) != 0) {
+    return fail(LTX25_E_INVAL, "a bf16 adapter matrix is not 2-byte aligned");
+  }
+  const int bits = w != nullptr && w->quantized ? w->bits : 16;
+  FoldPlan f = plan_fold(M, K, N, rank, bits, cu_count_hint(), x, y);
+  if (f.takes) {
+    // the linear's own checks (shape, weight, bias, epilogue, alignment)
+    // before any device use: a dry run of its plan
+    if (x == nullptr || y == nullptr) { return fail(LTX25_E_INVAL, "x or y is null"); }
+    int rc = check_qweight(w, K);
+    if (rc != LTX25_OK) { return rc; }
+    if (!bias_ok(bias, bias_dtype)) {
+      return fail(LTX25_E_INVAL, "bias dtype %d is not valid for a %s bias", bias_dtype,
+                  bias == nullptr ? "null" : "non-null");
+    }
+    if (epilogue != LTX25_EPI_NONE && epilogue != LTX25_EPI_GELU_TANH) {
+      return fail(LTX25_E_INVAL, "unknown epilogue %d", epilogue);
+    }
+    if ((rc = check_aligned("weight", w->codes)) != LTX25_OK) { return rc; }
+    DeviceState* ds = nullptr;
+    rc = current_device(&ds);
+    if (rc != LTX25_OK) { return rc; }
+    if (ds->cu_count != cu_count_hint()) {
+      f = plan_fold(M, K, N, rank, bits, ds->cu_count, x, y);
+    }
+    if (f.takes) {
+      return run_fold(ds, st, f, x, w, bias, bias_dtype, a, b, rank, y, M, K, N, epilogue);
+    }
+  }
+  // The reference's order: the linear, the adapter on its output, then the
+  // GELU (src/ltx25-block-metal.cc:639-645).
+  int rc = run_linear(st, x, w, bias, bias_dtype, y, M, K, N, LTX25_EPI_NONE);
+  if (rc != LTX25_OK) { return rc; }
+  rc = ltx25_lora_add(stream, x, a, b, y, nullptr, nullptr, M, K, N, rank);
+  if (rc != LTX25_OK) { return rc; }
+  if (epilogue == LTX25_EPI_GELU_TANH) { return ltx25_gelu_tanh(stream, y, y, (size_t)M * N); }
+  if (epilogue != LTX25_EPI_NONE) { return fail(LTX25_E_INVAL, "unknown epilogue %d", epilogue); }
   return LTX25_OK;
 }
 

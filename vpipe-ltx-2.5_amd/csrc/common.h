@@ -95,6 +95,15 @@ __device__ __forceinline__ float load_bias(const void* bias, int type, int n)
 // (bits 8 or 4, `group` 32 or 64) or dense bf16 (bits 16).
 struct GemmDesc {
   const uint16_t* x = nullptr;
+  // A two-part activation (the LoRA fold, dense weights on the 256 x 256
+  // and 128 x 128 tiles): columns [0, kx) of X are x [M][kx], columns
+  // [kx, K) are x2 [M][K - kx]; kx a multiple of 64. Null x2: X = x [M][K].
+  const uint16_t* x2 = nullptr;
+  int kx = 0;
+  // Rows of the weight present in memory (0: all N); rows past it read as
+  // zeros (the 256 x 256 and 128 x 128 tiles). The fold's r GEMM reads A
+  // [rank][K] as a [rk][K] weight this way.
+  int wn = 0;
   const void* w = nullptr;          // u8/u32 codes, or bf16 dense
   const uint16_t* scales = nullptr;
   const uint16_t* qbias = nullptr;
@@ -155,11 +164,12 @@ hipError_t launch_lora(const uint16_t* x, const uint16_t* a, const uint16_t* b,
                        uint16_t* y, int M, int K, int N, int rank, int ldb,
                        bool vec, int cu_count, hipStream_t stream,
                        const uint16_t* r_in = nullptr);
-// B [rows][cols] (row stride ld_src) -> [rows][ld_dst] with zero columns past
-// `cols`: the vector path's copy of an adapter whose rank is not a multiple
-// of 8.
+// B [rows][cols] (row stride ld_src) -> `width` columns of each dst row
+// (row stride ld_dst; width 0 = ld_dst) with zeros past `cols`: the vector
+// path's copy of an adapter whose rank is not a multiple of 8, and the
+// folded linear's weight tail.
 hipError_t launch_lora_pad(const uint16_t* src, int rows, int cols, int ld_src, uint16_t* dst,
-                           int ld_dst, hipStream_t stream);
+                           int ld_dst, hipStream_t stream, int width = 0);
 
 hipError_t launch_bias_add(uint16_t* y, const void* bias, int bias_type,
                            int M, int N, hipStream_t stream);
@@ -168,9 +178,13 @@ hipError_t launch_gelu(const uint16_t* x, uint16_t* y, size_t n,
 // y [tokens][heads][head_dim] bf16 *= 2 sigmoid(logits [tokens][heads] bf16), in place.
 hipError_t launch_gate_heads(uint16_t* y, const uint16_t* logits, int heads, int tokens,
                              int head_dim, hipStream_t stream);
+// codes -> bf16 [N][K] at output row stride ldo (0 = K); with `tail`,
+// columns [K, ldo) of row n are tail [n][0, tail_cols) (row stride
+// tail_ld) and zeros after them
 hipError_t launch_dequant(const void* codes, const uint16_t* scales,
                           const uint16_t* qbias, int bits, int group,
-                          uint16_t* out, int N, int K, hipStream_t stream);
+                          uint16_t* out, int N, int K, hipStream_t stream, int ldo = 0,
+                          const uint16_t* tail = nullptr, int tail_cols = 0, int tail_ld = 0);
 hipError_t launch_quantize_affine(const float* w, uint32_t* codes,
                                   uint16_t* scales, uint16_t* qbias, int N,
                                   int K, int bits, int group,

@@ -107,7 +107,7 @@ template <int BITS>
 __global__ void __launch_bounds__(kBlock)
 dequant_kernel(const uint8_t* codes, const uint16_t* scales,
                const uint16_t* qbias, int gshift, int gcols, uint16_t* out,
-               int N, int K)
+               int N, int K, int ldo, const uint16_t* tail, int tail_cols, int tail_ld)
 {
   const int n = blockIdx.x;
   const int runs = K >> 3;
@@ -115,7 +115,20 @@ dequant_kernel(const uint8_t* codes, const uint16_t* scales,
   const uint8_t* crow = codes + (size_t)n * K * BITS / 8;
   const uint16_t* srow = scales + (size_t)n * gcols;
   const uint16_t* qrow = qbias + (size_t)n * gcols;
-  uint16_t* orow = out + (size_t)n * K;
+  uint16_t* orow = out + (size_t)n * ldo;
+  // columns [K, ldo) of the row: tail row n (tail_cols of it, zeros past them)
+  if (tail != nullptr && blockIdx.y == 0 && (int)threadIdx.x < (ldo - K) / 8) {
+    const int c = (int)threadIdx.x * 8;
+    const uint16_t* trow = tail + (size_t)n * tail_ld;
+    uint32_t w[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t lo = c + 2 * t < tail_cols ? trow[c + 2 * t] : 0u;
+      const uint32_t hi = c + 2 * t + 1 < tail_cols ? trow[c + 2 * t + 1] : 0u;
+      w[t] = lo | (hi << 16);
+    }
+    *(uint4*)(orow + K + c) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
   uint32_t v[kDeqRuns][2];
   float s[kDeqRuns], b[kDeqRuns];
 #pragma unroll
@@ -293,18 +306,26 @@ hipError_t launch_gate_heads(uint16_t* y, const uint16_t* logits, int heads, int
 
 hipError_t launch_dequant(const void* codes, const uint16_t* scales,
                           const uint16_t* qbias, int bits, int group,
-                          uint16_t* out, int N, int K, hipStream_t stream)
+                          uint16_t* out, int N, int K, hipStream_t stream, int ldo,
+                          const uint16_t* tail, int tail_cols, int tail_ld)
 {
+  if (ldo == 0) { ldo = K; }
+  if (ldo < K || ldo % 8 != 0 || (ldo - K) / 8 > kBlock ||
+      (tail != nullptr && (tail_cols > ldo - K || tail_ld < tail_cols))) {
+    return hipErrorInvalidValue;
+  }
   const int gshift = ilog2(group);
   const int gcols = K / group;
   const int parts = (K / 8 + kBlock * kDeqRuns - 1) / (kBlock * kDeqRuns);
   const dim3 grid((unsigned)N, (unsigned)parts, 1);
   if (bits == 8) {
     hipLaunchKernelGGL(dequant_kernel<8>, grid, dim3(kBlock), 0, stream,
-                       (const uint8_t*)codes, scales, qbias, gshift, gcols, out, N, K);
+                       (const uint8_t*)codes, scales, qbias, gshift, gcols, out, N, K, ldo,
+                       tail, tail_cols, tail_ld);
   } else {
     hipLaunchKernelGGL(dequant_kernel<4>, grid, dim3(kBlock), 0, stream,
-                       (const uint8_t*)codes, scales, qbias, gshift, gcols, out, N, K);
+                       (const uint8_t*)codes, scales, qbias, gshift, gcols, out, N, K, ldo,
+                       tail, tail_cols, tail_ld);
   }
   return hipGetLastError();
 }

@@ -383,14 +383,16 @@ hipError_t launch_rb(const LoraParams& p, bool vec, dim3 grid, hipStream_t strea
   return hipGetLastError();
 }
 
-// dst[r][c] = c < cols ? src[r][c] : 0 for c < ld_dst (ld_dst % 8 == 0): an
-// adapter matrix with its rank padded, so the vector paths can load it. One
+// dst[r * ld_dst + c] = c < cols ? src[r][c] : 0 for c < width (width and
+// ld_dst multiples of 8): an adapter matrix with its rank padded, so the
+// vector paths can load it, or written into a wider matrix's last columns
+// (the folded linear's weight tail). One
 // thread per 8 destination elements (one 16-byte store); the source side
 // reads 16 bytes at once when its row start and stride allow it.
 __global__ void lora_pad_kernel(const uint16_t* __restrict__ src, int rows, int cols,
-                                int ld_src, uint16_t* __restrict__ dst, int ld_dst)
+                                int ld_src, uint16_t* __restrict__ dst, int ld_dst, int width)
 {
-  const size_t chunks = (size_t)ld_dst / 8;
+  const size_t chunks = (size_t)width / 8;
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (size_t)rows * chunks) { return; }
   const size_t r = i / chunks;
@@ -415,13 +417,16 @@ __global__ void lora_pad_kernel(const uint16_t* __restrict__ src, int rows, int 
 }  // namespace
 
 hipError_t launch_lora_pad(const uint16_t* src, int rows, int cols, int ld_src, uint16_t* dst,
-                           int ld_dst, hipStream_t stream)
+                           int ld_dst, hipStream_t stream, int width)
 {
-  if (ld_dst % 8 != 0 || ((uintptr_t)dst & 15u) != 0) { return hipErrorInvalidValue; }
-  const size_t n = (size_t)rows * (ld_dst / 8);
+  if (width == 0) { width = ld_dst; }
+  if (ld_dst % 8 != 0 || width % 8 != 0 || width > ld_dst || ((uintptr_t)dst & 15u) != 0) {
+    return hipErrorInvalidValue;
+  }
+  const size_t n = (size_t)rows * (width / 8);
   if (n == 0) { return hipSuccess; }
   lora_pad_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(src, rows, cols, ld_src, dst,
-                                                                     ld_dst);
+                                                                     ld_dst, width);
   return hipGetLastError();
 }
 

@@ -114,6 +114,18 @@ public:
   {
     return ltx25_lora_on_matrix_cores(M, K, N, rank) != 0;
   }
+  // A linear and its adapter as one call (the adapter before the GELU when
+  // `gelu`): a call site's linear + lora_ pair (src/ltx25-block-metal.cc:
+  // 428-436, 523-524, 639-648), folded into the GEMM where it can be.
+  void linear_lora(hipStream_t enc, const void* x, const QWeight& w, const void* bias,
+                   const void* a, const void* b, int rank, void* y, int M, int K, int N,
+                   bool gelu = false) const
+  {
+    const ltx25_qweight cw = to_c(w);
+    note(ltx25_linear_q_lora(enc, x, &cw, bias, bias != nullptr ? LTX25_DT_BF16 : LTX25_DT_NONE,
+                             a, b, rank, y, M, K, N,
+                             gelu ? LTX25_EPI_GELU_TANH : LTX25_EPI_NONE));
+  }
 
   // The dequant-once arm (src/ltx25-metal-ops.cc:467-502): LTX25_DEQUANT_ONCE_*.
   void set_dequant_once(int mode) { note(ltx25_set_dequant_once(mode)); }

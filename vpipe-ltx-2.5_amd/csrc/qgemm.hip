@@ -52,6 +52,9 @@ constexpr int kLdsRow = kBK + 8;    // bf16 per LDS row: 144 B pitch keeps
 
 struct KParams {
   const uint16_t* x;
+  const uint16_t* x2;      // FOLD: columns [kx, K) of the activation, [M][K - kx]
+  int wn;                  // weight rows in memory (<= N); rows past them read as zeros
+  int kx;                  // FOLD: columns of x (a multiple of kBK); else K
   const int8_t* xq;        // int8 activations (kI8Ops)
   const float* sx;         // per-row activation scales (kI8Ops)
   const float* sw;         // per-column weight scales (kI8Ops)
@@ -128,7 +131,7 @@ __device__ __forceinline__ void interleave()
   interleave_seq<NM, NR, NW, NV, NG>(std::make_integer_sequence<int, NM>{});
 }
 
-template <int BM, int BN, int WM, int WN, int BITS, bool SPLIT, int NS = 0>
+template <int BM, int BN, int WM, int WN, int BITS, bool SPLIT, int NS = 0, bool FOLD = false>
 __global__ void __launch_bounds__(WM * WN * 64)
 qgemm_kernel(KParams p)
 {
@@ -179,10 +182,12 @@ qgemm_kernel(KParams p)
   // Buffer resources and per-thread byte offsets, fixed for the whole loop;
   // each step adds a uniform K offset (an SGPR).
   const size_t wrow_bytes = (size_t)p.K * (QUANT ? BITS : (I8 ? 8 : 16)) / 8;
+  // FOLD: the activation is [x | x2], x with kx columns, x2 with K - kx
+  const int kx = FOLD ? p.kx : p.K;
   const __amdgpu_buffer_rsrc_t xr =
-      make_rsrc(I8 ? (const void*)p.xq : (const void*)p.x, (size_t)p.M * p.K * XB);
+      make_rsrc(I8 ? (const void*)p.xq : (const void*)p.x, (size_t)p.M * kx * XB);
   const __amdgpu_buffer_rsrc_t wr =
-      make_rsrc(QUANT || I8 ? (const void*)p.wq : (const void*)p.wd, (size_t)p.N * wrow_bytes);
+      make_rsrc(QUANT || I8 ? (const void*)p.wq : (const void*)p.wd, (size_t)p.wn * wrow_bytes);
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(p.scales, (size_t)p.N * p.gcols * 2);
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(p.qbias, (size_t)p.N * p.gcols * 2);
   uint32_t a_off[A_LD];
@@ -190,7 +195,16 @@ qgemm_kernel(KParams p)
   uint32_t s_off[B_LD];
 #pragma unroll
   for (int i = 0; i < A_LD; ++i) {
-    a_off[i] = (uint32_t)((size_t)(m0 + a_r + A_RSTEP * i) * p.K * XB + a_c * 16);
+    a_off[i] = (uint32_t)((size_t)(m0 + a_r + A_RSTEP * i) * kx * XB + a_c * 16);
+  }
+  const int kx2 = FOLD ? p.K - kx : 0;
+  const __amdgpu_buffer_rsrc_t xr2 = make_rsrc(p.x2, FOLD ? (size_t)p.M * kx2 * XB : 0);
+  uint32_t a_off2[FOLD ? A_LD : 1];
+  if constexpr (FOLD) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      a_off2[i] = (uint32_t)((size_t)(m0 + a_r + A_RSTEP * i) * kx2 * XB + a_c * 16);
+    }
   }
 #pragma unroll
   for (int i = 0; i < B_LD; ++i) {
@@ -205,8 +219,21 @@ qgemm_kernel(KParams p)
   uint16_t qraw[B_LD];
 
   auto load_a = [&](int k) {
+    if constexpr (FOLD) {
+      // The step's K range lies in one part. Selects, not a branch: a
+      // branch would split the step's scheduling regions (the issue
+      // pattern of interleave<> holds within one basic block).
+      const bool second = k >= kx;
+      const __amdgpu_buffer_rsrc_t r = second ? xr2 : xr;
+      const uint32_t so = (uint32_t)(second ? k - kx : k) * XB;
 #pragma unroll
-    for (int i = 0; i < A_LD; ++i) { areg[i] = buf_load16(xr, a_off[i], (uint32_t)k * XB); }
+      for (int i = 0; i < A_LD; ++i) {
+        areg[i] = buf_load16(r, second ? a_off2[i] : a_off[i], so);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_LD; ++i) { areg[i] = buf_load16(xr, a_off[i], (uint32_t)k * XB); }
+    }
   };
   auto load_b = [&](int k) {
 #pragma unroll
@@ -682,18 +709,21 @@ splitk_reduce_kernel(const float* partial, int splits, const void* bias,
 // Steps of the fully unrolled split-K slice (the audio shapes' K / 512).
 constexpr int kSplitSteps = 8;
 
-template <int BM, int BN, int WM, int WN, int BITS, bool SPLIT>
+template <int BM, int BN, int WM, int WN, int BITS, bool SPLIT, bool FOLD = false>
 hipError_t launch_cfg(const KParams& kp, int splits, hipStream_t stream)
 {
+  if constexpr (BITS == 16 && !FOLD) {
+    if (kp.x2 != nullptr) { return launch_cfg<BM, BN, WM, WN, BITS, SPLIT, true>(kp, splits, stream); }
+  }
   const dim3 grid((unsigned)(kp.tiles_m * kp.tiles_n), (unsigned)splits, 1);
   if constexpr (SPLIT && BITS != kI8Ops && BM == 128) {
     if (kp.k_chunk == kSplitSteps * kBK && kp.K % kp.k_chunk == 0) {
-      hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, BITS, SPLIT, kSplitSteps>), grid,
+      hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, BITS, SPLIT, kSplitSteps, FOLD>), grid,
                          dim3(WM * WN * 64), 0, stream, kp);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, BITS, SPLIT>), grid,
+  hipLaunchKernelGGL((qgemm_kernel<BM, BN, WM, WN, BITS, SPLIT, 0, FOLD>), grid,
                      dim3(WM * WN * 64), 0, stream, kp);
   return hipGetLastError();
 }
@@ -779,6 +809,7 @@ hipError_t launch_i8_gemm(const int8_t* xq, const float* sx, const int8_t* wq, c
   kp.y = y;
   kp.M = M;
   kp.N = N;
+  kp.wn = N;
   kp.K = K;
   kp.k_chunk = K;
   int dev = 0;
@@ -812,9 +843,16 @@ hipError_t launch_splitk_reduce(const float* partial, int splits, const void* bi
 hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
                        float* workspace, hipStream_t stream)
 {
+  if (d.x2 != nullptr &&
+      (plan.tile == 2 || d.bits != 16 || d.kx <= 0 || d.kx >= d.K || d.kx % kBK != 0)) {
+    return hipErrorInvalidValue;   // the two-part activation: dense weights, MFMA tiles
+  }
   if (plan.tile == 2) { return launch_skinny(d, plan, workspace, stream); }
   KParams kp = {};
   kp.x = d.x;
+  kp.x2 = d.x2;
+  kp.kx = d.x2 != nullptr ? d.kx : d.K;
+  kp.wn = d.wn > 0 && d.wn < d.N ? d.wn : d.N;
   kp.wq = (const uint8_t*)d.w;
   kp.wd = (const uint16_t*)d.w;
   kp.scales = d.scales;
