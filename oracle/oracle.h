@@ -21,6 +21,10 @@
  *   orc_quantize_affine              exact grid round trip, constant group,
  *                                    half-away rounding, clamp, error bound
  *   orc_dequant                      closed form fmaf(scale, q, bias)
+ *   orc_linear_f32_omp               numpy float64 within the f32 bound of
+ *                                    K products, thread-count invariant
+ *   orc_fill_normal                  seeded determinism, Kolmogorov-Smirnov
+ *                                    against N(0, 1), mean + stddev * z
  *   orc_linear_f64                   numpy float64 matmul, and bit-exact
  *                                    against the reference's own linear_
  *                                    (oracle/_ref, built from its sources)
@@ -45,6 +49,13 @@
  *   orc_i8_epilogue_ex               epilogue 0 equals orc_i8_epilogue; epilogue 1
  *                                    equals orc_i8_epilogue's f32 value through
  *                                    orc_gelu_tanh, then one bf16 rounding
+ * Two dequantized weights appear. orc_quantize_affine's `deq` is the
+ * reference test's CPU ground truth (scale * q, then + min: two f32
+ * roundings, tests/ltx25-qlinear-test.cc:93-141). orc_dequant is
+ * fmaf(scale, q, min) rounded once, then to bf16: the NORMATIVE weight of
+ * every GPU route, which the routes reproduce bit for bit. The two differ
+ * by at most one f32 ulp before the bf16 rounding; the GPU bars are set
+ * against orc_dequant's weight.
  * Not pinned against the reference: the exact output bits of libvpipe's
  * GEMM kernels and of its I8GemmContext (not present in the reference
  * tree), so parity there is against the closed-form semantics above.

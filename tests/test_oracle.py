@@ -185,6 +185,37 @@ def test_linear_f64_matches_numpy_float64():
     assert np.array_equal(orc.linear_f64(x, w, b), ours.astype(np.float32))
 
 
+def test_linear_f32_omp_matches_numpy_within_f32_accumulation():
+    """The timing baseline's f32 linear: the f64 result up to f32 rounding of
+    K products and sums, any thread count the same, bias added, W not
+    transposed."""
+    rng = np.random.default_rng(16)
+    x = rng.standard_normal((11, 300)).astype(np.float32)
+    w = rng.standard_normal((17, 300)).astype(np.float32)
+    b = rng.standard_normal(17).astype(np.float32)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T + b
+    bound = 300 * np.finfo(np.float32).eps * (np.abs(x).astype(np.float64) @
+                                             np.abs(w).astype(np.float64).T + np.abs(b))
+    one = orc.linear_f32_omp(x, w, b, threads=1)
+    assert np.all(np.abs(one - ref) <= bound)
+    assert np.array_equal(orc.linear_f32_omp(x, w, b, threads=4), one)
+    assert np.max(np.abs(orc.linear_f32_omp(x, w, None, threads=2) - (ref - b))) < 1e-3
+
+
+def test_fill_normal_is_seeded_standard_normal():
+    """The synthetic-data generator: a pure function of the seed, N(0, 1) by
+    a Kolmogorov-Smirnov test, and mean / stddev applied as mean + stddev z."""
+    from scipy import stats
+
+    a = orc.fill_normal(200000, 7)
+    assert np.array_equal(a, orc.fill_normal(200000, 7))
+    assert not np.array_equal(a, orc.fill_normal(200000, 8))
+    assert stats.kstest(a.astype(np.float64), "norm").pvalue > 1e-3
+    assert abs(float(a.mean())) < 0.01 and abs(float(a.std()) - 1.0) < 0.01
+    s = orc.fill_normal(1000, 7, 3.0, 0.5)
+    assert np.allclose(s, 3.0 + 0.5 * a[:1000], rtol=0, atol=2e-6)
+
+
 def test_gelu_matches_torch_tanh_gelu():
     x = np.concatenate([np.linspace(-12, 12, 20001), [0.0, -0.0, 1e-30, -1e-30, 50, -50]])
     x = x.astype(np.float32)
