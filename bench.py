@@ -639,10 +639,13 @@ def pmc_summary(fetch_csv, write_csv, cmd):
     w_fac = COPY_BYTES / (wr[cal][2] * 1024)
     groups = {}
     for i, (name, grid, v) in fe.items():
-        if ("qgemm_kernel" not in name and "splitk_reduce" not in name and
+        if "Cijk_" in name:
+            short = "hipBLASLt " + name    # the same-tensor comparison leg
+        elif ("qgemm_kernel" not in name and "splitk_reduce" not in name and
                 "dequant_kernel" not in name):
             continue
-        short = name[name.index("ltx25::"):].split("(ltx25")[0].replace("(anonymous namespace)::", "")
+        else:
+            short = name[name.index("ltx25::"):].split("(ltx25")[0].replace("(anonymous namespace)::", "")
         g = groups.setdefault((short, grid), [0, 0.0, 0.0])
         g[0] += 1
         g[1] += v * 1024 * f_fac
@@ -668,6 +671,10 @@ def pmc_summary(fetch_csv, write_csv, cmd):
              "|---|---|---|---|---|---|"]
     ffn = []
     for (short, grid), (n, fb, wb) in sorted(groups.items(), key=lambda kv: -kv[1][1] / kv[1][0]):
+        if short.startswith("hipBLASLt"):
+            lines.append(f"| `{short}` | {grid} | {n} | {fb / n / 1e6:.1f} | {wb / n / 1e6:.1f} | "
+                         f"up and down mixed (the same tensors as the dense GEMM) |")
+            continue
         which = ffn_grid.get(grid) if "256, 256" in short else None
         dense = ", 16, " in short
         a = (f"{alg(which, dense)[0] / 1e6:.1f} / {alg(which, dense)[1] / 1e6:.1f} ({which})"
@@ -709,10 +716,13 @@ def busy_summary(csv_path, out, cmd):
     with open(csv_path) as f:
         for r in csv.DictReader(f):
             name = r["Kernel_Name"]
-            if "ltx25::" not in name:
+            if "ltx25::" in name:
+                short = name[name.index("ltx25::"):].replace("(anonymous namespace)::", "")
+                short = short.split("(")[0]
+            elif "Cijk_" in name:
+                short = "hipBLASLt " + name    # the same-tensor comparison leg
+            else:
                 continue
-            short = name[name.index("ltx25::"):].replace("(anonymous namespace)::", "")
-            short = short.split("(")[0]
             key = (short, int(r["Grid_Size"]))
             d = per.setdefault(key, {"dur": {}, "c": {}})
             i = int(r["Dispatch_Id"])
@@ -772,6 +782,38 @@ def kernel_summary(db, out, cmd, note):
     print("\n".join(lines))
 
 
+def kernel_grid_summary(trace_csv, out, cmd, note):
+    """rocprofv3 kernel_trace.csv -> markdown per (kernel, grid): one row per
+    launch shape, so the four audio GEMMs and the plain reads of their byte
+    counts read separately."""
+    import csv
+    import statistics
+
+    groups = {}
+    with open(trace_csv) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"].replace("(anonymous namespace)::", "")
+            name = name.split("(")[0] if "(" in name else name
+            name = name if len(name) <= 90 else name[:90] + "..."
+            key = (name, int(r.get("Grid_Size", r.get("Grid_Size_X", 0))))
+            groups.setdefault(key, []).append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = [f"# Kernel stats per launch shape: {note}", "", "Commands (MI355X box, repo root):",
+             "", "```", cmd,
+             f"python3 bench.py --kernel-grid-summary <out>/run_kernel_trace.csv {out} '<cmd>' "
+             "'<note>'", "```", "",
+             "| kernel | grid (threads) | calls | median us | mean us | min us |",
+             "|---|---|---|---|---|---|"]
+    for (name, grid), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        if len(v) < 4:
+            continue
+        lines.append(f"| `{name}` | {grid} | {len(v)} | {statistics.median(v):.1f} | "
+                     f"{statistics.mean(v):.1f} | {min(v):.1f} |")
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -791,6 +833,8 @@ def main():
     ap.add_argument("--profile-copy", action="store_true",
                     help="also run one plain 256 MiB device copy, the known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--kernel-grid-summary", nargs=4, metavar=("TRACE_CSV", "OUT_MD", "CMD", "NOTE"),
+                    help="write a per-launch-shape kernel table from a rocprofv3 kernel trace")
     ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "CMD"),
                     help="summarise two rocprofv3 --pmc counter files into profiles/ and exit")
     ap.add_argument("--kernel-summary", nargs=4, metavar=("DB", "OUT_MD", "CMD", "NOTE"),
@@ -805,13 +849,16 @@ def main():
     if args.kernel_summary:
         kernel_summary(*args.kernel_summary)
         return
+    if args.kernel_grid_summary:
+        kernel_grid_summary(*args.kernel_grid_summary)
+        return
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: this build's path runs on a single MI355X; "
-              "multi-GPU sharding is a design note only (see DESIGN.md). Run with --gpus 1.",
+              "the multi-GPU sharding is designed but not built. Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 
