@@ -7,9 +7,11 @@
 //          (the video GEMMs, thousands of tokens); two waves per SIMD,
 //          so one wave's LDS / barrier / load waits are covered by the
 //          other's MFMAs
-//   skinny BM x BN = 128 x 128, 4 waves in 2 x 2, 64 x 64 per wave,
-//          with split-K across workgroups (the audio GEMMs at ~126 tokens
-//          and anything else too small to fill 256 CUs)
+//   mid    BM x BN = 128 x 128, 4 waves in 2 x 2, 64 x 64 per wave,
+//          with split-K across workgroups (more than 128 tokens but fewer
+//          256 x 256 tiles than CUs, and the calls of at most 128 tokens
+//          whose weight is too large for the M <= 128 kernel of skinny.hip,
+//          which takes the audio GEMMs)
 //
 // Per K step of 64 (one w8g64 group):
 //   - X rows stream from HBM as 16-byte loads into registers, then to LDS;
@@ -42,7 +44,7 @@ constexpr int kTallWM = 2;
 constexpr int kTallWN = 4;
 // Width of the small tile (128 rows; four waves, 2 x 2 at 128 columns or
 // 4 x 1 at 64).
-constexpr int kSkinnyBN = 128;
+constexpr int kMidBN = 128;
 constexpr int kBK = 64;             // K per main-loop step (bf16 activations)
 // BITS value of the int8 x int8 -> int32 GEMM (the int8 tier): both
 // operands are int8 rows, 128 of K per step in the same 128-byte LDS rows.
@@ -776,7 +778,7 @@ GemmPlan plan_gemm(int M, int N, int K, int bits, int cu_count, int force)
     return plan;
   }
   plan.tile = 1;
-  const long tiles = (long)((M + 127) / 128) * ((N + kSkinnyBN - 1) / kSkinnyBN);
+  const long tiles = (long)((M + 127) / 128) * ((N + kMidBN - 1) / kMidBN);
   // Split K until the workgroups cover the CUs once, with at least 512 of K
   // per split: each split writes a full f32 partial of the output. A sweep
   // over M = 256..2048, K = 2048 / 4096, N = 2048..16384 measured this
@@ -870,13 +872,13 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
   kp.bias_type = d.bias != nullptr ? d.bias_type : kBiasNone;
   kp.epilogue = d.epilogue;
   const int bm = plan.tile == 0 ? 256 : 128;
-  const int bn = plan.tile == 0 ? 256 : kSkinnyBN;
+  const int bn = plan.tile == 0 ? 256 : kMidBN;
   kp.tiles_m = (d.M + bm - 1) / bm;
   kp.tiles_n = (d.N + bn - 1) / bn;
 
   hipError_t e = plan.tile == 0
                      ? launch_tile<256, 256, kTallWM, kTallWN>(kp, d.bits, plan.splits, stream)
-                     : launch_tile<128, kSkinnyBN, 2 * 128 / kSkinnyBN, kSkinnyBN / 64>(
+                     : launch_tile<128, kMidBN, 2 * 128 / kMidBN, kMidBN / 64>(
                            kp, d.bits, plan.splits, stream);
   if (e != hipSuccess || plan.splits <= 1) { return e; }
   return launch_splitk_reduce(workspace, plan.splits, kp.bias, kp.bias_type, d.epilogue, d.y_in,
