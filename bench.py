@@ -641,8 +641,8 @@ def pmc_summary(fetch_csv, write_csv, cmd):
     for i, (name, grid, v) in fe.items():
         if "Cijk_" in name:
             short = "hipBLASLt " + name    # the same-tensor comparison leg
-        elif ("qgemm_kernel" not in name and "splitk_reduce" not in name and
-                "dequant_kernel" not in name):
+        elif ("qgemm_kernel" not in name and "tall_dense_kernel" not in name and
+                "splitk_reduce" not in name and "dequant_kernel" not in name):
             continue
         else:
             short = name[name.index("ltx25::"):].split("(ltx25")[0].replace("(anonymous namespace)::", "")
@@ -675,8 +675,9 @@ def pmc_summary(fetch_csv, write_csv, cmd):
             lines.append(f"| `{short}` | {grid} | {n} | {fb / n / 1e6:.1f} | {wb / n / 1e6:.1f} | "
                          f"up and down mixed (the same tensors as the dense GEMM) |")
             continue
-        which = ffn_grid.get(grid) if "256, 256" in short else None
-        dense = ", 16, " in short
+        tall_dense = "tall_dense_kernel" in short   # the 256 x 256 dense tile (tall.hip)
+        which = ffn_grid.get(grid) if "256, 256" in short or tall_dense else None
+        dense = ", 16, " in short or tall_dense
         a = (f"{alg(which, dense)[0] / 1e6:.1f} / {alg(which, dense)[1] / 1e6:.1f} ({which})"
              if which else "")
         lines.append(f"| `{short}` | {grid} | {n} | {fb / n / 1e6:.1f} | {wb / n / 1e6:.1f} | {a} |")
@@ -705,7 +706,8 @@ def busy_summary(csv_path, out, cmd):
     run with GRBM_GUI_ACTIVE, SQ_VALU_MFMA_BUSY_CYCLES and TCC_BUSY_avr.
     GRBM_GUI_ACTIVE counts the graphics engine's active cycles summed over
     the 8 XCDs, so /8 / duration is the clock; SQ_VALU_MFMA_BUSY_CYCLES sums
-    the busy cycles of every SIMD (32 per v_mfma_f32_32x32x16_bf16), so
+    the busy cycles of every SIMD (32 per v_mfma_f32_32x32x16_bf16, 16 per
+    v_mfma_f32_16x16x32_bf16), so
     dividing by the SIMD count (4 per CU) x the active cycles gives the
     fraction of the elapsed time the matrix cores ran; TCC_BUSY_avr is the
     mean busy cycles of an L2 channel."""
@@ -936,8 +938,8 @@ def main():
         "pct_bf16_peak": round(100 * ffn["tflops"] / PEAK_BF16_TFLOPS, 2),
         "ffn": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in ffn.items()},
         "roofline": {
-            "kernel": ("qgemm_kernel<256,256,2,4,16,false> (dense GEMM of the dequant-once route; "
-                       "up with GELU and down)" if ffn["route"] != "fused" else
+            "kernel": ("tall_dense_kernel (the 256x256 dense GEMM on 16x16x32 MFMAs, "
+                       "dequant-once route; up with GELU and down)" if ffn["route"] != "fused" else
                        "qgemm_kernel<256,256,2,4,8,false> (up with GELU and down)"),
             "bound": "mfma",
             "achieved": round(achieved, 2),

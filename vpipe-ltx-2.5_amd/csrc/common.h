@@ -139,6 +139,11 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
 bool plan_skinny(int M, int N, int K, int bits, int cu_count, GemmPlan& plan);
 hipError_t launch_skinny(const GemmDesc& d, const GemmPlan& plan, float* workspace,
                          hipStream_t stream);
+// The dense bf16 GEMM of the 256 x 256 tile on v_mfma_f32_16x16x32_bf16
+// (tall.hip): the dequant-once arm and dense weights, without a two-part
+// activation or y_in, N % 8 == 0. launch_gemm routes there when it takes.
+bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan);
+hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream);
 // The no-allocation linear's split-K scratch (noalloc.hip): a fixed device
 // array of kNoAllocScratchBytes per GPU. noalloc_scratch() returns the
 // current device's copy, resolving its address on the first call there.

@@ -1,0 +1,314 @@
+// The dense bf16 GEMM of the 256 x 256 tile: y = x . w^T (+ bias) (+ GELU),
+// for the dequant-once arm of the quantized linear (the weight expanded to
+// bf16 once per call) and for dense weights. Same tile, operand feed and
+// epilogue as the template in qgemm.hip, with v_mfma_f32_16x16x32_bf16
+// instead of 32x32x16: with identical LDS traffic the 16x16x32 main loop runs
+// ~10% faster on this GPU, and its sums come out bit-identical to the
+// 32x32x16 tile's (the fused-dequant route, which stays on the template).
+//
+//   - 8 waves in 2 x 4, 128 x 64 of the output per wave: 8 x 4 blocks of
+//     16 x 16, 128 f32 accumulators per lane;
+//   - a 64-deep K step is two 32-deep slices, each run in two halves of 16
+//     MFMAs (A blocks 0..3, then 4..7); the next half's fragments are read
+//     under the current half's MFMAs (A double-buffered per half, B per
+//     slice: 64 registers);
+//   - X and W rows arrive as whole 128-byte row segments (16-byte loads, 8
+//     lanes per row) in registers and are written a step later to one of two
+//     LDS stages; each register is reloaded a quarter step after its LDS
+//     write, which gives every load a step to land;
+//   - LDS rows are 160 bytes: a 16x16x32 fragment read covers 16 rows x 4
+//     pieces of 16 bytes, and at this pitch those 64 pieces fall in distinct
+//     banks (at the template's 144 bytes they do not: the tile measured 1e8
+//     bank-conflict cycles per launch there, 1.3e6 here). Two stages fill the
+//     160 KB of LDS; the bias sits in the row pads of the last 32 W rows of
+//     stage 1, which neither the operand rows nor the staged output reach;
+//   - one barrier per step; bias, GELU-tanh and one rounding to bf16 in the
+//     epilogue, staged in LDS and stored as 16-byte row segments.
+//
+// Reference semantics: MetalOps::dequant_mma_ -> dense_mma_
+// (src/ltx25-metal-ops.cc:467-502, 342-465), then bias_add (:568).
+#include "common.h"
+
+#include <type_traits>
+#include <utility>
+
+namespace ltx25 {
+namespace {
+
+constexpr int kBM = 256;
+constexpr int kBN = 256;
+constexpr int kThreads = 512;
+constexpr int kBK = 64;
+constexpr int kRow = kBK + 16;               // bf16 per LDS row (160 bytes)
+constexpr int kSide = 256 * kRow;            // one operand's rows in a stage
+constexpr int kStage = 2 * kSide;
+constexpr int kLd = 4;                       // 16-byte loads per thread per operand and step
+constexpr int kEP = kBN + 8;                 // bf16 per staged output row
+constexpr int kLdsHalfs = 2 * kStage;        // 163840 bytes
+static_assert(kBM * kEP <= kLdsHalfs, "the staged tile fits the stages");
+// bias value c: row 480 + c / 8 of stage 1 (its last 32 W rows), pad float c % 8
+constexpr int kBiasRow = kStage + 480 * kRow + kBK;
+static_assert(kBiasRow >= kBM * kEP, "the bias pads lie past the staged tile");
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+struct TallParams {
+  const uint16_t* x;
+  const uint16_t* w;
+  const void* bias;
+  uint16_t* y;
+  int M, N, K;
+  int wn;                  // rows of w in memory; rows past them read as zeros
+  int bias_type, epilogue;
+  int tiles_m, tiles_n;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, size_t bytes)
+{
+  // loads past `bytes` return zeros: rows past M and past wn
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)(uint32_t)bytes,
+                                           0x00020000);
+}
+
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>): the
+// index is a compile-time constant inside f
+template <typename F, int... I>
+__device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I...>)
+{
+  (f(std::integral_constant<int, I>{}), ...);
+}
+
+template <int N, typename F>
+__device__ __forceinline__ void unroll(F&& f)
+{
+  unroll_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+tall_dense_kernel(TallParams p)
+{
+  __shared__ __attribute__((aligned(16))) uint16_t lds[kLdsHalfs];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 2;
+  const int wn = wave & 3;
+  int tm, tn;
+  map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * kBM;
+  const int n0 = tn * kBN;
+  const int nsteps = p.K / kBK;
+  auto bias_at = [&](int c) -> float* { return (float*)(lds + kBiasRow + (c / 8) * kRow) + (c & 7); };
+
+  if (tid < kBN) {
+    const int n = n0 + tid;
+    *bias_at(tid) = n < p.N ? load_bias(p.bias, p.bias_type, n) : 0.0f;
+  }
+
+  // thread t loads rows t / 8 + 64 i of the X and of the W tile, 16-byte
+  // piece t % 8 of the step's 128 bytes
+  const int lr = tid >> 3;
+  const int lc = tid & 7;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, (size_t)p.M * p.K * 2);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (size_t)p.wn * p.K * 2);
+  uint32_t xoff[kLd], woff[kLd];
+#pragma unroll
+  for (int i = 0; i < kLd; ++i) {
+    xoff[i] = (uint32_t)(m0 + lr + 64 * i) * (uint32_t)p.K * 2u + (uint32_t)lc * 16u;
+    woff[i] = (uint32_t)(n0 + lr + 64 * i) * (uint32_t)p.K * 2u + (uint32_t)lc * 16u;
+  }
+  const int dst = lr * kRow + lc * 8;
+  uint4 xreg[kLd], wreg[kLd];
+  auto load_x = [&](int k, int i) {
+    xreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff[i], k * 2, 0));
+  };
+  auto load_w = [&](int k, int i) {
+    wreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woff[i], k * 2, 0));
+  };
+  auto store_x = [&](int st, int i) { *(uint4*)(lds + st * kStage + dst + 64 * i * kRow) = xreg[i]; };
+  auto store_w = [&](int st, int i) {
+    *(uint4*)(lds + st * kStage + kSide + dst + 64 * i * kRow) = wreg[i];
+  };
+
+  // fragments of a 16 x 32 operand block b: lane l holds row 16 b + l % 16,
+  // K 32 slice + 8 (l / 16) .. + 7
+  const int fa = (wm * 128 + (lane & 15)) * kRow + (lane >> 4) * 8;
+  const int fb = kSide + (wn * 64 + (lane & 15)) * kRow + (lane >> 4) * 8;
+  bf16x8 afr[2][4];   // [half parity]: A blocks 4 h .. 4 h + 3
+  bf16x8 bfr[2][4];   // [slice parity]: the slice's 4 B blocks
+  auto rd_a = [&](int st, int sl, int hh, int buf, int i) {
+    afr[buf][i] = *(const bf16x8*)(lds + st * kStage + fa + (4 * hh + i) * 16 * kRow + sl * 32);
+  };
+  auto rd_b = [&](int st, int sl, int buf, int j) {
+    bfr[buf][j] = *(const bf16x8*)(lds + st * kStage + fb + j * 16 * kRow + sl * 32);
+  };
+  f32x4v acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) { acc[i][j][r] = 0.0f; }
+    }
+  }
+
+  // prologue: step 0 into stage 0, step 1 into registers, the first fragments
+#pragma unroll
+  for (int i = 0; i < kLd; ++i) {
+    load_x(0, i);
+    load_w(0, i);
+  }
+#pragma unroll
+  for (int i = 0; i < kLd; ++i) {
+    store_x(0, i);
+    store_w(0, i);
+  }
+  if (nsteps > 1) {
+#pragma unroll
+    for (int i = 0; i < kLd; ++i) {
+      load_x(kBK, i);
+      load_w(kBK, i);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    rd_a(0, 0, 0, 0, i);
+    rd_b(0, 0, 0, i);
+  }
+
+  // Step s reads stage s & 1 in four quarters (slice q / 2, half q % 2) of
+  // 16 MFMAs. Reads for the next quarter in its first gaps: q0 A half 1 of
+  // slice 0; q1 A half 0 and B of slice 1; q2 A half 1 of slice 1; q3 (after
+  // the barrier) A half 0 and B of slice 0 of step s + 1. Writes of step
+  // s + 1 to the other stage: X in q0, W in q2; each register is reloaded
+  // with step s + 2 one quarter after its write (X in q1, W in q3). Every
+  // instruction sits in its own gap between MFMAs (the scheduling barriers
+  // hold the order).
+  auto step = [&](int s, auto do_store, auto do_load) {
+    constexpr bool kStore = decltype(do_store)::value;
+    constexpr bool kLoad = decltype(do_load)::value;
+    const int st = s & 1;
+    const int nst = st ^ 1;
+    unroll<4>([&](auto qq) {
+      constexpr int q = decltype(qq)::value;
+      constexpr int sl = q >> 1;
+      constexpr int hh = q & 1;
+      constexpr int abuf = q & 1;
+      constexpr int bbuf = sl & 1;
+      if constexpr (q == 3) {
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's writes and reads done
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      unroll<16>([&](auto gg) {
+        constexpr int g = decltype(gg)::value;
+        constexpr int i = g / 4;
+        constexpr int j = g % 4;
+        acc[4 * hh + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[bbuf][j], afr[abuf][i],
+                                                                     acc[4 * hh + i][j], 0, 0, 0);
+        if constexpr (q == 0 && g < 4) { rd_a(st, 0, 1, abuf ^ 1, g); }
+        if constexpr (q == 1 && g < 4) { rd_a(st, 1, 0, abuf ^ 1, g); }
+        if constexpr (q == 1 && g >= 4 && g < 8) { rd_b(st, 1, bbuf ^ 1, g - 4); }
+        if constexpr (q == 2 && g < 4) { rd_a(st, 1, 1, abuf ^ 1, g); }
+        if constexpr (kStore && q == 3 && g < 4) { rd_a(nst, 0, 0, abuf ^ 1, g); }
+        if constexpr (kStore && q == 3 && g >= 4 && g < 8) { rd_b(nst, 0, bbuf ^ 1, g - 4); }
+        // operand writes and reloads at gaps 8, 10, 12, 14
+        constexpr bool io_gap = g >= 8 && (g & 1) == 0;
+        constexpr int li = (g - 8) / 2;
+        if constexpr (kStore && q == 0 && io_gap) { store_x(nst, li); }
+        if constexpr (kLoad && q == 1 && io_gap) { load_x((s + 2) * kBK, li); }
+        if constexpr (kStore && q == 2 && io_gap) { store_w(nst, li); }
+        if constexpr (kLoad && q == 3 && io_gap) { load_w((s + 2) * kBK, li); }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    });
+  };
+  // the last two steps are peeled: no loads past the end, no writes after it
+  int s = 0;
+  for (; s + 2 < nsteps; ++s) { step(s, std::true_type{}, std::true_type{}); }
+  if (s + 1 < nsteps) {
+    step(s, std::true_type{}, std::false_type{});
+    ++s;
+  }
+  step(s, std::false_type{}, std::false_type{});
+  __syncthreads();   // every wave is done reading the operand stages
+
+  // Accumulator block (i, j), lane l, register r (the MFMAs take the weight
+  // fragment first): row 16 i + l % 16 of the wave's rows, column
+  // 16 j + 4 (l / 16) + r of its columns -- four consecutive columns.
+  const int lrow = lane & 15;
+  const int lcol = (lane >> 4) * 4;
+  uint16_t* const stage = lds;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = wn * 64 + j * 16 + lcol;
+    const f32x4 b4 = *(const f32x4*)bias_at(c);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = wm * 128 + i * 16 + lrow;
+      float v[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        v[t] = acc[i][j][t] + b4[t];
+        if (p.epilogue == kEpiGelu) { v[t] = gelu_tanh(v[t]); }
+      }
+      *(uint2*)(stage + r * kEP + c) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+  }
+  __syncthreads();
+  constexpr int CPR = kBN / 8;   // 16-byte chunks per output row
+#pragma unroll 4
+  for (int q = tid; q < kBM * CPR; q += kThreads) {
+    const int r = q / CPR;
+    const int c = (q % CPR) * 8;
+    const int m = m0 + r;
+    const int n = n0 + c;
+    if (m >= p.M || n >= p.N) { continue; }
+    const uint4 v = *(const uint4*)(stage + r * kEP + c);
+    // non-temporal: the tile is not read again by this launch
+    __builtin_nontemporal_store(__builtin_bit_cast(i32x4, v), (i32x4*)(p.y + (size_t)m * p.N + n));
+  }
+}
+
+}  // namespace
+
+bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan)
+{
+  // The template keeps the two-part activation, the accumulating output and
+  // rows that are not whole 16-byte chunks. The per-lane byte offsets are
+  // 32-bit, rows past the last tile's end included.
+  constexpr size_t kFourGib = (size_t)1 << 32;
+  return plan.tile == 0 && plan.splits == 1 && d.bits == 16 && d.x2 == nullptr &&
+         d.y_in == nullptr && d.N % 8 == 0 && d.K % kBK == 0 && d.K >= kBK &&
+         (size_t)(d.M + kBM) * d.K * 2 < kFourGib && (size_t)(d.N + kBN) * d.K * 2 < kFourGib;
+}
+
+hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream)
+{
+  constexpr size_t kTwoGib = (size_t)1 << 31;
+  if (d.M < 1 || d.N < 8 || d.N % 8 != 0 || d.K < kBK || d.K % kBK != 0 || d.bits != 16 ||
+      (size_t)d.M * d.K * 2 >= kTwoGib || (size_t)d.N * d.K * 2 >= kTwoGib ||
+      (size_t)d.M * d.N * 2 >= kTwoGib) {
+    return hipErrorInvalidValue;
+  }
+  TallParams p;
+  p.x = d.x;
+  p.w = (const uint16_t*)d.w;
+  p.bias = d.bias;
+  p.y = d.y;
+  p.M = d.M;
+  p.N = d.N;
+  p.K = d.K;
+  p.wn = d.wn > 0 && d.wn < d.N ? d.wn : d.N;
+  p.bias_type = d.bias != nullptr ? d.bias_type : kBiasNone;
+  p.epilogue = d.epilogue;
+  p.tiles_m = (d.M + kBM - 1) / kBM;
+  p.tiles_n = (d.N + kBN - 1) / kBN;
+  hipLaunchKernelGGL(tall_dense_kernel, dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(kThreads), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace ltx25
