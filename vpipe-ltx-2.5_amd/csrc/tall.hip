@@ -14,8 +14,9 @@
 //     slice: 64 registers);
 //   - X and W rows arrive as whole 128-byte row segments (16-byte loads, 8
 //     lanes per row) in registers and are written a step later to one of two
-//     LDS stages; each register is reloaded a quarter step after its LDS
-//     write, which gives every load a step to land;
+//     LDS stages, X in the first quarter of a step, W in the second; each
+//     register is reloaded right after its LDS write, which gives every load
+//     a step to land;
 //   - LDS rows are 160 bytes: a 16x16x32 fragment read covers 16 rows x 4
 //     pieces of 16 bytes, and at this pitch those 64 pieces fall in distinct
 //     banks (at the template's 144 bytes they do not: the tile measured 1e8
@@ -182,8 +183,10 @@ tall_dense_kernel(TallParams p)
   // 16 MFMAs. Reads for the next quarter in its first gaps: q0 A half 1 of
   // slice 0; q1 A half 0 and B of slice 1; q2 A half 1 of slice 1; q3 (after
   // the barrier) A half 0 and B of slice 0 of step s + 1. Writes of step
-  // s + 1 to the other stage: X in q0, W in q2; each register is reloaded
-  // with step s + 2 one quarter after its write (X in q1, W in q3). Every
+  // s + 1 to the other stage: X in q0, W in q1, each register reloaded with
+  // step s + 2 in the gap after its write, so a load has a whole step to
+  // land and the writes have drained before the barrier's lgkmcnt(0) (with
+  // the W writes in q2 the wait before the barrier cost FFN down 6%). Every
   // instruction sits in its own gap between MFMAs (the scheduling barriers
   // hold the order).
   auto step = [&](int s, auto do_store, auto do_load) {
@@ -214,13 +217,14 @@ tall_dense_kernel(TallParams p)
         if constexpr (q == 2 && g < 4) { rd_a(st, 1, 1, abuf ^ 1, g); }
         if constexpr (kStore && q == 3 && g < 4) { rd_a(nst, 0, 0, abuf ^ 1, g); }
         if constexpr (kStore && q == 3 && g >= 4 && g < 8) { rd_b(nst, 0, bbuf ^ 1, g - 4); }
-        // operand writes and reloads at gaps 8, 10, 12, 14
-        constexpr bool io_gap = g >= 8 && (g & 1) == 0;
+        // operand writes at gaps 8, 10, 12, 14, reloads at 9, 11, 13, 15
+        constexpr bool wr_gap = g >= 8 && (g & 1) == 0;
+        constexpr bool ld_gap = g >= 8 && (g & 1) == 1;
         constexpr int li = (g - 8) / 2;
-        if constexpr (kStore && q == 0 && io_gap) { store_x(nst, li); }
-        if constexpr (kLoad && q == 1 && io_gap) { load_x((s + 2) * kBK, li); }
-        if constexpr (kStore && q == 2 && io_gap) { store_w(nst, li); }
-        if constexpr (kLoad && q == 3 && io_gap) { load_w((s + 2) * kBK, li); }
+        if constexpr (kStore && q == 0 && wr_gap) { store_x(nst, li); }
+        if constexpr (kLoad && q == 0 && ld_gap) { load_x((s + 2) * kBK, li); }
+        if constexpr (kStore && q == 1 && wr_gap) { store_w(nst, li); }
+        if constexpr (kLoad && q == 1 && ld_gap) { load_w((s + 2) * kBK, li); }
         __builtin_amdgcn_sched_barrier(0);
       });
     });
