@@ -111,6 +111,40 @@ def test_i8_gemm_bit_exact(pkg, M, K, N, bias_kind):
     assert np.array_equal(host_bits(y), y_ref)
 
 
+@pytest.mark.parametrize("M,K,N,bias_kind", [
+    (4100, 1152, 4104, "bf16"),   # 17 x 17 tiles, ragged in M and N: the 256 x 256 int8 tile
+    (4100, 1152, 4100, "f32"),    # N % 8 != 0: the template's 256 x 256 tile
+    (2304, 640, 8192, "none"),    # 9 x 32 tiles, 5 K steps of 128
+])
+def test_i8_gemm_tall_tiles_bit_exact(pkg, M, K, N, bias_kind):
+    """Shapes whose 256 x 256 tiles fill the GPU: int32 accumulators equal to an exact
+    float64 GEMM of the same operands on every row, and every bf16 output equal to the
+    oracle's epilogue over those accumulators."""
+    say(f"i8 gemm (256 x 256 tiles) M={M} K={K} N={N} bias={bias_kind}")
+    rng = np.random.default_rng(38)
+    xq_h = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    wq_h = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    sx_h = (rng.random(M) * 0.05).astype(np.float32)
+    sw_h = (rng.random(N) * 0.001).astype(np.float32)
+    bias_h = rng_normal(rng, (N,), 0.5)
+    if bias_kind == "none":
+        bias_dev, bdt, bias_o = None, 0, None
+    elif bias_kind == "f32":
+        bias_dev, bdt, bias_o = dev_f32(bias_h), 2, bias_h
+    else:
+        bb = orc.bf16_rne(bias_h)
+        bias_dev, bdt, bias_o = dev_bf16(bb), 1, bb
+    xq, wq = torch.from_numpy(xq_h).cuda(), torch.from_numpy(wq_h).cuda()
+    y, acc = i8_run(pkg, xq, dev_f32(sx_h), wq, dev_f32(sw_h), bias_dev, M, K, N)
+    exact = xq.double() @ wq.double().t()
+    assert torch.equal(acc.double(), exact)
+    del exact
+    acc_h = acc.cpu().numpy()
+    assert np.array_equal(host_bits(y), orc.i8_epilogue(acc_h, sx_h, sw_h, bias_o, bdt))
+    # a small corner of the accumulators against the oracle's own int32 GEMM
+    assert np.array_equal(acc_h[-40:, -24:], orc.i8_gemm_i32(xq_h[-40:], wq_h[-24:]))
+
+
 @pytest.mark.parametrize("N", [4096, 16384])
 def test_config3_video_shape(pkg, N):
     say(f"config 3: i8 8160x4096->{N}")

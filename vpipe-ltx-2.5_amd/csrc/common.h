@@ -144,6 +144,13 @@ hipError_t launch_skinny(const GemmDesc& d, const GemmPlan& plan, float* workspa
 // activation or y_in, N % 8 == 0. launch_gemm routes there when it takes.
 bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan);
 hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream);
+// The int8 tier's GEMM on the same tile (tall.hip, v_mfma_i32_16x16x64_i8):
+// N % 8 == 0, K a multiple of 128. launch_i8_gemm routes there when the
+// 256 x 256 tiles fill the GPU and it takes the shape.
+bool tall_i8_takes(int M, int N, int K);
+hipError_t launch_tall_i8(const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
+                          const void* bias, int bias_type, int epilogue, uint16_t* y,
+                          int32_t* acc, int M, int K, int N, hipStream_t stream);
 // The no-allocation linear's split-K scratch (noalloc.hip): a fixed device
 // array of kNoAllocScratchBytes per GPU. noalloc_scratch() returns the
 // current device's copy, resolving its address on the first call there.

@@ -821,7 +821,11 @@ hipError_t launch_i8_gemm(const int8_t* xq, const float* sx, const int8_t* wq, c
     cus = 256;
   }
   // the tall tile when it fills the GPU, else 128 x 128
-  if ((long)((M + 255) / 256) * ((N + 255) / 256) >= cus) {
+  const bool fills = (long)((M + 255) / 256) * ((N + 255) / 256) >= cus;
+  if (fills && tall_i8_takes(M, N, K)) {
+    return launch_tall_i8(xq, sx, wq, sw, bias, kp.bias_type, epilogue, y, acc, M, K, N, stream);
+  }
+  if (fills) {
     kp.tiles_m = (M + 255) / 256;
     kp.tiles_n = (N + 255) / 256;
     return launch_cfg<256, 256, kTallWM, kTallWN, kI8Ops, false>(kp, 1, stream);

@@ -1,10 +1,16 @@
-// The dense bf16 GEMM of the 256 x 256 tile: y = x . w^T (+ bias) (+ GELU),
-// for the dequant-once arm of the quantized linear (the weight expanded to
-// bf16 once per call) and for dense weights. Same tile, operand feed and
-// epilogue as the template in qgemm.hip, with v_mfma_f32_16x16x32_bf16
-// instead of 32x32x16: with identical LDS traffic the 16x16x32 main loop runs
-// ~10% faster on this GPU, and its sums come out bit-identical to the
-// 32x32x16 tile's (the fused-dequant route, which stays on the template).
+// The 256 x 256 GEMM tile on the 16-row MFMAs, in two operand modes:
+//   - bf16: y = x . w^T (+ bias) (+ GELU) on v_mfma_f32_16x16x32_bf16, for
+//     the dequant-once arm of the quantized linear (the weight expanded to
+//     bf16 once per call) and for dense weights. Same tile, operand feed and
+//     epilogue as the template in qgemm.hip, with 16x16x32 instead of
+//     32x32x16: with identical LDS traffic the 16x16x32 main loop runs ~10%
+//     faster on this GPU, and its sums come out bit-identical to the
+//     32x32x16 tile's (the fused-dequant route, which stays on the template);
+//   - int8: the int8 tier's GEMM, int8 x int8 -> exact int32 on
+//     v_mfma_i32_16x16x64_i8, 128 of K per step in the same 128-byte row
+//     segments (so every fragment offset is the bf16 mode's), epilogue
+//     y = bf16(epi(fma(float(acc), sx[m] * sw[n], bias[n] or +0))) in that
+//     order, as the template's int8 mode computes it.
 //
 //   - 8 waves in 2 x 4, 128 x 64 of the output per wave: 8 x 4 blocks of
 //     16 x 16, 128 f32 accumulators per lane;
@@ -27,7 +33,8 @@
 //     epilogue, staged in LDS and stored as 16-byte row segments.
 //
 // Reference semantics: MetalOps::dequant_mma_ -> dense_mma_
-// (src/ltx25-metal-ops.cc:467-502, 342-465), then bias_add (:568).
+// (src/ltx25-metal-ops.cc:467-502, 342-465), then bias_add (:568); the int8
+// mode is the tier under dense_mma_ (I8GemmContext::gemm, :386-391).
 #include "common.h"
 
 #include <type_traits>
@@ -39,26 +46,37 @@ namespace {
 constexpr int kBM = 256;
 constexpr int kBN = 256;
 constexpr int kThreads = 512;
-constexpr int kBK = 64;
-constexpr int kRow = kBK + 16;               // bf16 per LDS row (160 bytes)
+constexpr int kSB = 128;                     // bytes of each row per K step
+constexpr int kBK = 64;                      // bf16 per step (the int8 mode: 128 int8)
+constexpr int kRow = kBK + 16;               // halfs per LDS row (160 bytes)
 constexpr int kSide = 256 * kRow;            // one operand's rows in a stage
 constexpr int kStage = 2 * kSide;
 constexpr int kLd = 4;                       // 16-byte loads per thread per operand and step
 constexpr int kEP = kBN + 8;                 // bf16 per staged output row
 constexpr int kLdsHalfs = 2 * kStage;        // 163840 bytes
 static_assert(kBM * kEP <= kLdsHalfs, "the staged tile fits the stages");
-// bias value c: row 480 + c / 8 of stage 1 (its last 32 W rows), pad float c % 8
-constexpr int kBiasRow = kStage + 480 * kRow + kBK;
-static_assert(kBiasRow >= kBM * kEP, "the bias pads lie past the staged tile");
+// Epilogue constants in the 32-byte row pads of stage 1's last W rows (the
+// operand rows use bytes 0..127 of a row; the staged output tile ends
+// before them): bias value c at row 480 + c / 8, pad float c % 8; the int8
+// mode's sw[n0 + c] at rows 448.., sx[m0 + r] at rows 416..
+constexpr int kPadRow(int first) { return kStage + first * kRow + kBK; }
+static_assert(kPadRow(416) >= kBM * kEP, "the epilogue pads lie past the staged tile");
+
+constexpr int kModeBf16 = 0;
+constexpr int kModeI8 = 1;
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef int i32x4v __attribute__((ext_vector_type(4)));
 
 struct TallParams {
-  const uint16_t* x;
-  const uint16_t* w;
+  const void* x;           // bf16 [M][K] or int8 [M][K]
+  const void* w;           // bf16 [N][K] or int8 [N][K]
   const void* bias;
+  const float* sx;         // int8 mode: per-row activation scales
+  const float* sw;         // int8 mode: per-column weight scales
+  int32_t* acc_out;        // int8 mode, optional: the raw int32 accumulators
   uint16_t* y;
-  int M, N, K;
+  int M, N, K;             // K in elements
   int wn;                  // rows of w in memory; rows past them read as zeros
   int bias_type, epilogue;
   int tiles_m, tiles_n;
@@ -85,9 +103,12 @@ __device__ __forceinline__ void unroll(F&& f)
   unroll_seq(f, std::make_integer_sequence<int, N>{});
 }
 
+template <int MODE>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-tall_dense_kernel(TallParams p)
+tall_kernel(TallParams p)
 {
+  constexpr bool I8 = MODE == kModeI8;
+  constexpr int kEB = I8 ? 1 : 2;   // bytes per operand element
   __shared__ __attribute__((aligned(16))) uint16_t lds[kLdsHalfs];
 
   const int tid = threadIdx.x;
@@ -99,60 +120,79 @@ tall_dense_kernel(TallParams p)
   map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
   const int m0 = tm * kBM;
   const int n0 = tn * kBN;
-  const int nsteps = p.K / kBK;
-  auto bias_at = [&](int c) -> float* { return (float*)(lds + kBiasRow + (c / 8) * kRow) + (c & 7); };
+  const uint32_t row_bytes = (uint32_t)p.K * kEB;
+  const int nsteps = (int)(row_bytes / kSB);
+  auto pad_at = [&](int first, int c) -> float* {
+    return (float*)(lds + kPadRow(first) + (c / 8) * kRow) + (c & 7);
+  };
 
   if (tid < kBN) {
     const int n = n0 + tid;
-    *bias_at(tid) = n < p.N ? load_bias(p.bias, p.bias_type, n) : 0.0f;
+    *pad_at(480, tid) = n < p.N ? load_bias(p.bias, p.bias_type, n) : 0.0f;
+    if constexpr (I8) {
+      const int m = m0 + tid;
+      *pad_at(448, tid) = n < p.N ? p.sw[n] : 0.0f;
+      *pad_at(416, tid) = m < p.M ? p.sx[m] : 0.0f;
+    }
   }
 
   // thread t loads rows t / 8 + 64 i of the X and of the W tile, 16-byte
   // piece t % 8 of the step's 128 bytes
   const int lr = tid >> 3;
   const int lc = tid & 7;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, (size_t)p.M * p.K * 2);
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (size_t)p.wn * p.K * 2);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, (size_t)p.M * row_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (size_t)p.wn * row_bytes);
   uint32_t xoff[kLd], woff[kLd];
 #pragma unroll
   for (int i = 0; i < kLd; ++i) {
-    xoff[i] = (uint32_t)(m0 + lr + 64 * i) * (uint32_t)p.K * 2u + (uint32_t)lc * 16u;
-    woff[i] = (uint32_t)(n0 + lr + 64 * i) * (uint32_t)p.K * 2u + (uint32_t)lc * 16u;
+    xoff[i] = (uint32_t)(m0 + lr + 64 * i) * row_bytes + (uint32_t)lc * 16u;
+    woff[i] = (uint32_t)(n0 + lr + 64 * i) * row_bytes + (uint32_t)lc * 16u;
   }
   const int dst = lr * kRow + lc * 8;
   uint4 xreg[kLd], wreg[kLd];
-  auto load_x = [&](int k, int i) {
-    xreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff[i], k * 2, 0));
+  // s: the step whose 128 bytes per row are loaded
+  auto load_x = [&](int s, int i) {
+    xreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff[i], s * kSB, 0));
   };
-  auto load_w = [&](int k, int i) {
-    wreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woff[i], k * 2, 0));
+  auto load_w = [&](int s, int i) {
+    wreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woff[i], s * kSB, 0));
   };
   auto store_x = [&](int st, int i) { *(uint4*)(lds + st * kStage + dst + 64 * i * kRow) = xreg[i]; };
   auto store_w = [&](int st, int i) {
     *(uint4*)(lds + st * kStage + kSide + dst + 64 * i * kRow) = wreg[i];
   };
 
-  // fragments of a 16 x 32 operand block b: lane l holds row 16 b + l % 16,
-  // K 32 slice + 8 (l / 16) .. + 7
+  // fragments of a 16-row operand block b and a 64-byte K slice: lane l
+  // holds row 16 b + l % 16, bytes 16 (l / 16) .. + 15 of the slice (8 bf16
+  // of a 16x16x32 MFMA, 16 int8 of a 16x16x64 one)
   const int fa = (wm * 128 + (lane & 15)) * kRow + (lane >> 4) * 8;
   const int fb = kSide + (wn * 64 + (lane & 15)) * kRow + (lane >> 4) * 8;
-  bf16x8 afr[2][4];   // [half parity]: A blocks 4 h .. 4 h + 3
-  bf16x8 bfr[2][4];   // [slice parity]: the slice's 4 B blocks
+  i32x4v afr[2][4];   // [half parity]: A blocks 4 h .. 4 h + 3
+  i32x4v bfr[2][4];   // [slice parity]: the slice's 4 B blocks
   auto rd_a = [&](int st, int sl, int hh, int buf, int i) {
-    afr[buf][i] = *(const bf16x8*)(lds + st * kStage + fa + (4 * hh + i) * 16 * kRow + sl * 32);
+    afr[buf][i] = *(const i32x4v*)(lds + st * kStage + fa + (4 * hh + i) * 16 * kRow + sl * 32);
   };
   auto rd_b = [&](int st, int sl, int buf, int j) {
-    bfr[buf][j] = *(const bf16x8*)(lds + st * kStage + fb + j * 16 * kRow + sl * 32);
+    bfr[buf][j] = *(const i32x4v*)(lds + st * kStage + fb + j * 16 * kRow + sl * 32);
   };
-  f32x4v acc[8][4];
+  using AccT = std::conditional_t<I8, i32x4v, f32x4v>;
+  AccT acc[8][4];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) { acc[i][j][r] = 0.0f; }
+      for (int r = 0; r < 4; ++r) { acc[i][j][r] = 0; }
     }
   }
+  auto mfma = [&](const i32x4v& b, const i32x4v& a, AccT c) -> AccT {
+    if constexpr (I8) {
+      return __builtin_amdgcn_mfma_i32_16x16x64_i8(b, a, c, 0, 0, 0);
+    } else {
+      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, b),
+                                                     __builtin_bit_cast(bf16x8, a), c, 0, 0, 0);
+    }
+  };
 
   // prologue: step 0 into stage 0, step 1 into registers, the first fragments
 #pragma unroll
@@ -168,8 +208,8 @@ tall_dense_kernel(TallParams p)
   if (nsteps > 1) {
 #pragma unroll
     for (int i = 0; i < kLd; ++i) {
-      load_x(kBK, i);
-      load_w(kBK, i);
+      load_x(1, i);
+      load_w(1, i);
     }
   }
   __syncthreads();
@@ -209,8 +249,7 @@ tall_dense_kernel(TallParams p)
         constexpr int g = decltype(gg)::value;
         constexpr int i = g / 4;
         constexpr int j = g % 4;
-        acc[4 * hh + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[bbuf][j], afr[abuf][i],
-                                                                     acc[4 * hh + i][j], 0, 0, 0);
+        acc[4 * hh + i][j] = mfma(bfr[bbuf][j], afr[abuf][i], acc[4 * hh + i][j]);
         if constexpr (q == 0 && g < 4) { rd_a(st, 0, 1, abuf ^ 1, g); }
         if constexpr (q == 1 && g < 4) { rd_a(st, 1, 0, abuf ^ 1, g); }
         if constexpr (q == 1 && g >= 4 && g < 8) { rd_b(st, 1, bbuf ^ 1, g - 4); }
@@ -222,9 +261,9 @@ tall_dense_kernel(TallParams p)
         constexpr bool ld_gap = g >= 8 && (g & 1) == 1;
         constexpr int li = (g - 8) / 2;
         if constexpr (kStore && q == 0 && wr_gap) { store_x(nst, li); }
-        if constexpr (kLoad && q == 0 && ld_gap) { load_x((s + 2) * kBK, li); }
+        if constexpr (kLoad && q == 0 && ld_gap) { load_x(s + 2, li); }
         if constexpr (kStore && q == 1 && wr_gap) { store_w(nst, li); }
-        if constexpr (kLoad && q == 1 && ld_gap) { load_w((s + 2) * kBK, li); }
+        if constexpr (kLoad && q == 1 && ld_gap) { load_w(s + 2, li); }
         __builtin_amdgcn_sched_barrier(0);
       });
     });
@@ -248,14 +287,35 @@ tall_dense_kernel(TallParams p)
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = wn * 64 + j * 16 + lcol;
-    const f32x4 b4 = *(const f32x4*)bias_at(c);
+    const f32x4 b4 = *(const f32x4*)pad_at(480, c);
+    f32x4 sw4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (I8) { sw4 = *(const f32x4*)pad_at(448, c); }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = wm * 128 + i * 16 + lrow;
       float v[4];
+      if constexpr (I8) {
+        const float sxm = *pad_at(416, r);
+        const int m = m0 + r;
+        const int n = n0 + c;
+        if (p.acc_out != nullptr && m < p.M && n < p.N) {
+          // the raw int32 accumulators, when asked for (bit-exact checks);
+          // N % 8 == 0, so the four columns are all in range
+          int32_t* arow = p.acc_out + (size_t)m * p.N + n;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) { arow[t] = acc[i][j][t]; }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          // y = bf16(fma(float(acc), sx[m] * sw[n], bias[n])), that order
+          v[t] = fmaf((float)acc[i][j][t], sxm * sw4[t], b4[t]);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) { v[t] = acc[i][j][t] + b4[t]; }
+      }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        v[t] = acc[i][j][t] + b4[t];
         if (p.epilogue == kEpiGelu) { v[t] = gelu_tanh(v[t]); }
       }
       *(uint2*)(stage + r * kEP + c) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
@@ -276,6 +336,20 @@ tall_dense_kernel(TallParams p)
   }
 }
 
+constexpr size_t kTwoGib = (size_t)1 << 31;
+constexpr size_t kFourGib = (size_t)1 << 32;
+
+hipError_t launch_tall(const TallParams& p, int mode, hipStream_t stream)
+{
+  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
+  if (mode == kModeI8) {
+    hipLaunchKernelGGL(tall_kernel<kModeI8>, grid, dim3(kThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(tall_kernel<kModeBf16>, grid, dim3(kThreads), 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan)
@@ -283,7 +357,6 @@ bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan)
   // The template keeps the two-part activation, the accumulating output and
   // rows that are not whole 16-byte chunks. The per-lane byte offsets are
   // 32-bit, rows past the last tile's end included.
-  constexpr size_t kFourGib = (size_t)1 << 32;
   return plan.tile == 0 && plan.splits == 1 && d.bits == 16 && d.x2 == nullptr &&
          d.y_in == nullptr && d.N % 8 == 0 && d.K % kBK == 0 && d.K >= kBK &&
          (size_t)(d.M + kBM) * d.K * 2 < kFourGib && (size_t)(d.N + kBN) * d.K * 2 < kFourGib;
@@ -291,15 +364,14 @@ bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan)
 
 hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream)
 {
-  constexpr size_t kTwoGib = (size_t)1 << 31;
   if (d.M < 1 || d.N < 8 || d.N % 8 != 0 || d.K < kBK || d.K % kBK != 0 || d.bits != 16 ||
       (size_t)d.M * d.K * 2 >= kTwoGib || (size_t)d.N * d.K * 2 >= kTwoGib ||
       (size_t)d.M * d.N * 2 >= kTwoGib) {
     return hipErrorInvalidValue;
   }
-  TallParams p;
+  TallParams p = {};
   p.x = d.x;
-  p.w = (const uint16_t*)d.w;
+  p.w = d.w;
   p.bias = d.bias;
   p.y = d.y;
   p.M = d.M;
@@ -310,9 +382,40 @@ hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream)
   p.epilogue = d.epilogue;
   p.tiles_m = (d.M + kBM - 1) / kBM;
   p.tiles_n = (d.N + kBN - 1) / kBN;
-  hipLaunchKernelGGL(tall_dense_kernel, dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(kThreads), 0,
-                     stream, p);
-  return hipGetLastError();
+  return launch_tall(p, kModeBf16, stream);
+}
+
+bool tall_i8_takes(int M, int N, int K)
+{
+  // 128 of K per step; the same 32-bit offset bound as the bf16 mode
+  return N % 8 == 0 && K % kSB == 0 && K >= kSB && (size_t)(M + kBM) * K < kFourGib &&
+         (size_t)(N + kBN) * K < kFourGib;
+}
+
+hipError_t launch_tall_i8(const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
+                          const void* bias, int bias_type, int epilogue, uint16_t* y,
+                          int32_t* acc, int M, int K, int N, hipStream_t stream)
+{
+  if (M < 1 || !tall_i8_takes(M, N, K) || (size_t)M * N * 2 >= kTwoGib) {
+    return hipErrorInvalidValue;
+  }
+  TallParams p = {};
+  p.x = xq;
+  p.w = wq;
+  p.sx = sx;
+  p.sw = sw;
+  p.acc_out = acc;
+  p.bias = bias;
+  p.y = y;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.wn = N;
+  p.bias_type = bias != nullptr ? bias_type : kBiasNone;
+  p.epilogue = epilogue;
+  p.tiles_m = (M + kBM - 1) / kBM;
+  p.tiles_n = (N + kBN - 1) / kBN;
+  return launch_tall(p, kModeI8, stream);
 }
 
 }  // namespace ltx25
