@@ -143,6 +143,10 @@ hipError_t launch_skinny(const GemmDesc& d, const GemmPlan& plan, float* workspa
 // (tall.hip): the dequant-once arm and dense weights, without a two-part
 // activation or y_in, N % 8 == 0. launch_gemm routes there when it takes.
 bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan);
+// The same tile with w8 codes (groups of 64 or 32) dequantized in registers
+// once per workgroup before the LDS write: bit-identical to the dense tile
+// over the dequant-once expansion. launch_tall_dense runs either.
+bool tall_w8_takes(const GemmDesc& d, const GemmPlan& plan);
 hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream);
 // The int8 tier's GEMM on the same tile (tall.hip, v_mfma_i32_16x16x64_i8):
 // N % 8 == 0, K a multiple of 128. launch_i8_gemm routes there when the

@@ -854,7 +854,7 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
     return hipErrorInvalidValue;   // the two-part activation: dense weights, MFMA tiles
   }
   if (plan.tile == 2) { return launch_skinny(d, plan, workspace, stream); }
-  if (tall_dense_takes(d, plan)) { return launch_tall_dense(d, stream); }
+  if (tall_dense_takes(d, plan) || tall_w8_takes(d, plan)) { return launch_tall_dense(d, stream); }
   KParams kp = {};
   kp.x = d.x;
   kp.x2 = d.x2;

@@ -64,6 +64,7 @@ static_assert(kPadRow(416) >= kBM * kEP, "the epilogue pads lie past the staged 
 
 constexpr int kModeBf16 = 0;
 constexpr int kModeI8 = 1;
+constexpr int kModeW8 = 2;
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef int i32x4v __attribute__((ext_vector_type(4)));
@@ -75,6 +76,9 @@ struct TallParams {
   const float* sx;         // int8 mode: per-row activation scales
   const float* sw;         // int8 mode: per-column weight scales
   int32_t* acc_out;        // int8 mode, optional: the raw int32 accumulators
+  const uint16_t* scales;  // w8 mode: bf16 [N][K / group]
+  const uint16_t* qbias;   // w8 mode: bf16 [N][K / group]
+  int gshift, gcols;       // w8 mode: log2(group), K / group
   uint16_t* y;
   int M, N, K;             // K in elements
   int wn;                  // rows of w in memory; rows past them read as zeros
@@ -108,7 +112,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 tall_kernel(TallParams p)
 {
   constexpr bool I8 = MODE == kModeI8;
-  constexpr int kEB = I8 ? 1 : 2;   // bytes per operand element
+  constexpr bool W8 = MODE == kModeW8;
+  constexpr int kEB = I8 ? 1 : 2;   // bytes per X element
   __shared__ __attribute__((aligned(16))) uint16_t lds[kLdsHalfs];
 
   const int tid = threadIdx.x;
@@ -141,13 +146,58 @@ tall_kernel(TallParams p)
   const int lr = tid >> 3;
   const int lc = tid & 7;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, (size_t)p.M * row_bytes);
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (size_t)p.wn * row_bytes);
+  const __amdgpu_buffer_rsrc_t wr =
+      make_rsrc(p.w, (size_t)p.wn * (W8 ? (uint32_t)p.K : row_bytes));
   uint32_t xoff[kLd], woff[kLd];
 #pragma unroll
   for (int i = 0; i < kLd; ++i) {
     xoff[i] = (uint32_t)(m0 + lr + 64 * i) * row_bytes + (uint32_t)lc * 16u;
     woff[i] = (uint32_t)(n0 + lr + 64 * i) * row_bytes + (uint32_t)lc * 16u;
   }
+  // w8 mode: thread t holds codes of weight rows t / 4 and t / 4 + 128,
+  // 16-byte piece t % 4 of the step's 64 codes (4 lanes cover a row's
+  // segment), and the scale and zero point of each piece's group; it
+  // dequantizes them in registers, exactly as the expansion kernel does
+  // (fma(scale, q, zero point) in f32, one rounding to bf16), and writes the
+  // 16 bf16 of each row to the row's 32-byte span of the stage.
+  const int cr = tid >> 2;
+  const int cp = tid & 3;
+  uint32_t coff[2] = {0u, 0u}, soff[2] = {0u, 0u};
+  __amdgpu_buffer_rsrc_t sr = wr, br = wr;
+  if constexpr (W8) {
+    sr = make_rsrc(p.scales, (size_t)p.wn * p.gcols * 2);
+    br = make_rsrc(p.qbias, (size_t)p.wn * p.gcols * 2);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      coff[i] = (uint32_t)(n0 + cr + 128 * i) * (uint32_t)p.K + (uint32_t)cp * 16u;
+      soff[i] = ((uint32_t)(n0 + cr + 128 * i) * (uint32_t)p.gcols +
+                 ((uint32_t)cp * 16u >> p.gshift)) * 2u;
+    }
+  }
+  const int gstep = W8 ? (kBK >> p.gshift) * 2 : 0;   // bytes of a scale row per step
+  uint4 creg[2];
+  uint32_t sreg[2], breg[2];
+  uint32_t dq[8];   // one row's 16 dequantized bf16
+  auto load_c = [&](int s, int i) {
+    creg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)coff[i], s * kBK, 0));
+  };
+  auto load_sb = [&](int s, int i) {
+    sreg[i] = __builtin_amdgcn_raw_buffer_load_b16(sr, (int)soff[i], s * gstep, 0);
+    breg[i] = __builtin_amdgcn_raw_buffer_load_b16(br, (int)soff[i], s * gstep, 0);
+  };
+  // codes 2 h and 2 h + 1 of row i's piece
+  auto dq_pair = [&](int i, int h) {
+    const float sc = __builtin_bit_cast(float, sreg[i] << 16);
+    const float zp = __builtin_bit_cast(float, breg[i] << 16);
+    const uint32_t w = creg[i][h >> 1];
+    const int sh = (h & 1) * 16;
+    dq[h] = pack_bf16x2(fmaf(sc, (float)((w >> sh) & 0xffu), zp),
+                        fmaf(sc, (float)((w >> (sh + 8)) & 0xffu), zp));
+  };
+  auto store_dq = [&](int st, int i, int hh) {
+    *(uint4*)(lds + st * kStage + kSide + (cr + 128 * i) * kRow + cp * 16 + 8 * hh) =
+        make_uint4(dq[4 * hh], dq[4 * hh + 1], dq[4 * hh + 2], dq[4 * hh + 3]);
+  };
   const int dst = lr * kRow + lc * 8;
   uint4 xreg[kLd], wreg[kLd];
   // s: the step whose 128 bytes per row are loaded
@@ -198,18 +248,56 @@ tall_kernel(TallParams p)
 #pragma unroll
   for (int i = 0; i < kLd; ++i) {
     load_x(0, i);
-    load_w(0, i);
+    if constexpr (!W8) { load_w(0, i); }
+  }
+  if constexpr (W8) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      load_c(0, i);
+      load_sb(0, i);
+    }
   }
 #pragma unroll
   for (int i = 0; i < kLd; ++i) {
     store_x(0, i);
-    store_w(0, i);
+    if constexpr (!W8) { store_w(0, i); }
+  }
+  if constexpr (W8) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int h = 0; h < 8; ++h) { dq_pair(i, h); }
+      store_dq(0, i, 0);
+      store_dq(0, i, 1);
+    }
   }
   if (nsteps > 1) {
+    // Step 1's loads in the main loop's issue order (X rows, then the
+    // weight's: rows, or codes then scale and zero point row by row). The
+    // loop's wait counts also cover its first iteration, so a prologue
+    // order that differs makes every iteration wait for more loads than
+    // its own order needs (X and W interleaved here once made each step's
+    // first X write wait for a W load issued three quarters earlier).
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < kLd; ++i) {
       load_x(1, i);
-      load_w(1, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (!W8) {
+#pragma unroll
+      for (int i = 0; i < kLd; ++i) {
+        load_w(1, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        load_c(1, i);
+        __builtin_amdgcn_sched_barrier(0);
+        load_sb(1, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
   __syncthreads();
@@ -262,8 +350,22 @@ tall_kernel(TallParams p)
         constexpr int li = (g - 8) / 2;
         if constexpr (kStore && q == 0 && wr_gap) { store_x(nst, li); }
         if constexpr (kLoad && q == 0 && ld_gap) { load_x(s + 2, li); }
-        if constexpr (kStore && q == 1 && wr_gap) { store_w(nst, li); }
-        if constexpr (kLoad && q == 1 && ld_gap) { load_w(s + 2, li); }
+        if constexpr (!W8) {
+          if constexpr (kStore && q == 1 && wr_gap) { store_w(nst, li); }
+          if constexpr (kLoad && q == 1 && ld_gap) { load_w(s + 2, li); }
+        } else {
+          // w8: row 0 dequantized in q0's second half, written in q1's
+          // first gaps; row 1 dequantized in q1 gaps 4..11, written at 12
+          // and 14; each row's codes reloaded right after its writes
+          if constexpr (kStore && q == 0 && g >= 8) { dq_pair(0, g - 8); }
+          if constexpr (kStore && q == 1 && (g == 0 || g == 2)) { store_dq(nst, 0, g / 2); }
+          if constexpr (kLoad && q == 1 && g == 1) { load_c(s + 2, 0); }
+          if constexpr (kLoad && q == 1 && g == 3) { load_sb(s + 2, 0); }
+          if constexpr (kStore && q == 1 && g >= 4 && g < 12) { dq_pair(1, g - 4); }
+          if constexpr (kStore && q == 1 && (g == 12 || g == 14)) { store_dq(nst, 1, (g - 12) / 2); }
+          if constexpr (kLoad && q == 1 && g == 13) { load_c(s + 2, 1); }
+          if constexpr (kLoad && q == 1 && g == 15) { load_sb(s + 2, 1); }
+        }
         __builtin_amdgcn_sched_barrier(0);
       });
     });
@@ -344,6 +446,8 @@ hipError_t launch_tall(const TallParams& p, int mode, hipStream_t stream)
   const dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
   if (mode == kModeI8) {
     hipLaunchKernelGGL(tall_kernel<kModeI8>, grid, dim3(kThreads), 0, stream, p);
+  } else if (mode == kModeW8) {
+    hipLaunchKernelGGL(tall_kernel<kModeW8>, grid, dim3(kThreads), 0, stream, p);
   } else {
     hipLaunchKernelGGL(tall_kernel<kModeBf16>, grid, dim3(kThreads), 0, stream, p);
   }
@@ -362,8 +466,43 @@ bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan)
          (size_t)(d.M + kBM) * d.K * 2 < kFourGib && (size_t)(d.N + kBN) * d.K * 2 < kFourGib;
 }
 
+bool tall_w8_takes(const GemmDesc& d, const GemmPlan& plan)
+{
+  // w8 codes with groups of 64 or 32 on the 256 x 256 plan; the codes'
+  // byte offsets are 32-bit like the activation's
+  return plan.tile == 0 && plan.splits == 1 && d.bits == 8 && (d.group == 64 || d.group == 32) &&
+         d.x2 == nullptr && d.y_in == nullptr && d.N % 8 == 0 && d.K % kBK == 0 && d.K >= kBK &&
+         (size_t)(d.M + kBM) * d.K * 2 < kFourGib && (size_t)(d.N + kBN) * d.K < kFourGib;
+}
+
 hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream)
 {
+  if (d.bits == 8) {
+    GemmPlan plan;
+    plan.tile = 0;
+    plan.splits = 1;
+    if (d.M < 1 || !tall_w8_takes(d, plan) || (size_t)d.M * d.N * 2 >= kTwoGib) {
+      return hipErrorInvalidValue;
+    }
+    TallParams p = {};
+    p.x = d.x;
+    p.w = d.w;
+    p.scales = d.scales;
+    p.qbias = d.qbias;
+    p.gshift = d.group == 64 ? 6 : 5;
+    p.gcols = d.K / d.group;
+    p.bias = d.bias;
+    p.y = d.y;
+    p.M = d.M;
+    p.N = d.N;
+    p.K = d.K;
+    p.wn = d.N;
+    p.bias_type = d.bias != nullptr ? d.bias_type : kBiasNone;
+    p.epilogue = d.epilogue;
+    p.tiles_m = (d.M + kBM - 1) / kBM;
+    p.tiles_n = (d.N + kBN - 1) / kBN;
+    return launch_tall(p, kModeW8, stream);
+  }
   if (d.M < 1 || d.N < 8 || d.N % 8 != 0 || d.K < kBK || d.K % kBK != 0 || d.bits != 16 ||
       (size_t)d.M * d.K * 2 >= kTwoGib || (size_t)d.N * d.K * 2 >= kTwoGib ||
       (size_t)d.M * d.N * 2 >= kTwoGib) {
