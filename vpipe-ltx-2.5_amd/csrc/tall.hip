@@ -20,7 +20,7 @@
 //     slice: 64 registers);
 //   - X and W rows arrive as whole 128-byte row segments (16-byte loads, 8
 //     lanes per row) in registers and are written a step later to one of two
-//     LDS stages, X in the first quarter of a step, W in the second; each
+//     LDS stages, W in the second quarter of a step, X in the third; each
 //     register is reloaded right after its LDS write, which gives every load
 //     a step to land;
 //   - LDS rows are 160 bytes: a 16x16x32 fragment read covers 16 rows x 4
@@ -279,11 +279,6 @@ tall_kernel(TallParams p)
     // its own order needs (X and W interleaved here once made each step's
     // first X write wait for a W load issued three quarters earlier).
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < kLd; ++i) {
-      load_x(1, i);
-      __builtin_amdgcn_sched_barrier(0);
-    }
     if constexpr (!W8) {
 #pragma unroll
       for (int i = 0; i < kLd; ++i) {
@@ -299,6 +294,11 @@ tall_kernel(TallParams p)
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+#pragma unroll
+    for (int i = 0; i < kLd; ++i) {
+      load_x(1, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -308,15 +308,17 @@ tall_kernel(TallParams p)
   }
 
   // Step s reads stage s & 1 in four quarters (slice q / 2, half q % 2) of
-  // 16 MFMAs. Reads for the next quarter in its first gaps: q0 A half 1 of
-  // slice 0; q1 A half 0 and B of slice 1; q2 A half 1 of slice 1; q3 (after
+  // 16 MFMAs. Fragment reads for later quarters: q0 A half 1 of slice 0 and
+  // B of slice 1; q1 A half 0 of slice 1; q2 A half 1 of slice 1; q3 (after
   // the barrier) A half 0 and B of slice 0 of step s + 1. Writes of step
-  // s + 1 to the other stage: X in q0, W in q1, each register reloaded with
+  // s + 1 to the other stage: W in q1, X in q2, each register reloaded with
   // step s + 2 in the gap after its write, so a load has a whole step to
-  // land and the writes have drained before the barrier's lgkmcnt(0) (with
-  // the W writes in q2 the wait before the barrier cost FFN down 6%). Every
-  // instruction sits in its own gap between MFMAs (the scheduling barriers
-  // hold the order).
+  // land. That puts eight LDS instructions in every quarter (with the B
+  // reads in q1 and the X writes in q0 the quarters carried 8 / 12 / 4 / 8,
+  // and the tile ran 0.6-1.4% slower on the FFN GEMMs in an interleaved
+  // A/B). The writes issue early enough to drain before the barrier's
+  // lgkmcnt(0). Every instruction sits in its own gap between MFMAs (the
+  // scheduling barriers hold the order).
   auto step = [&](int s, auto do_store, auto do_load) {
     constexpr bool kStore = decltype(do_store)::value;
     constexpr bool kLoad = decltype(do_load)::value;
@@ -339,17 +341,21 @@ tall_kernel(TallParams p)
         constexpr int j = g % 4;
         acc[4 * hh + i][j] = mfma(bfr[bbuf][j], afr[abuf][i], acc[4 * hh + i][j]);
         if constexpr (q == 0 && g < 4) { rd_a(st, 0, 1, abuf ^ 1, g); }
+        if constexpr (q == 0 && g >= 4 && g < 8) { rd_b(st, 1, 1, g - 4); }
         if constexpr (q == 1 && g < 4) { rd_a(st, 1, 0, abuf ^ 1, g); }
-        if constexpr (q == 1 && g >= 4 && g < 8) { rd_b(st, 1, bbuf ^ 1, g - 4); }
-        if constexpr (q == 2 && g < 4) { rd_a(st, 1, 1, abuf ^ 1, g); }
+        if constexpr (q == 2 && g >= 8 && g < 12) { rd_a(st, 1, 1, abuf ^ 1, g - 8); }
         if constexpr (kStore && q == 3 && g < 4) { rd_a(nst, 0, 0, abuf ^ 1, g); }
-        if constexpr (kStore && q == 3 && g >= 4 && g < 8) { rd_b(nst, 0, bbuf ^ 1, g - 4); }
-        // operand writes at gaps 8, 10, 12, 14, reloads at 9, 11, 13, 15
+        if constexpr (kStore && q == 3 && g >= 4 && g < 8) { rd_b(nst, 0, 0, g - 4); }
+        // W writes at gaps 8, 10, 12, 14 of q1, reloads at 9, 11, 13, 15;
+        // X writes at gaps 0, 2, 4, 6 of q2, reloads at 1, 3, 5, 7
         constexpr bool wr_gap = g >= 8 && (g & 1) == 0;
         constexpr bool ld_gap = g >= 8 && (g & 1) == 1;
         constexpr int li = (g - 8) / 2;
-        if constexpr (kStore && q == 0 && wr_gap) { store_x(nst, li); }
-        if constexpr (kLoad && q == 0 && ld_gap) { load_x(s + 2, li); }
+        constexpr bool xwr_gap = g < 8 && (g & 1) == 0;
+        constexpr bool xld_gap = g < 8 && (g & 1) == 1;
+        constexpr int xi = g / 2;
+        if constexpr (kStore && q == 2 && xwr_gap) { store_x(nst, xi); }
+        if constexpr (kLoad && q == 2 && xld_gap) { load_x(s + 2, xi); }
         if constexpr (!W8) {
           if constexpr (kStore && q == 1 && wr_gap) { store_w(nst, li); }
           if constexpr (kLoad && q == 1 && ld_gap) { load_w(s + 2, li); }
