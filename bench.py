@@ -703,7 +703,11 @@ def pmc_summary(fetch_csv, write_csv, cmd):
 
 def busy_summary(csv_path, out, cmd):
     """Shader clock, MFMA-busy and L2-busy per kernel from one rocprofv3 --pmc
-    run with GRBM_GUI_ACTIVE, SQ_VALU_MFMA_BUSY_CYCLES and TCC_BUSY_avr.
+    run with GRBM_GUI_ACTIVE, SQ_VALU_MFMA_BUSY_CYCLES and TCC_BUSY_avr, and,
+    when the run also counted them, the fraction of wave cycles spent waiting
+    on any instruction dependency (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES) and on
+    LDS instruction issue (SQ_WAIT_INST_LDS / SQ_WAVE_CYCLES), and the LDS
+    bank-conflict cycles per launch (SQ_LDS_BANK_CONFLICT, summed over CUs).
     GRBM_GUI_ACTIVE counts the graphics engine's active cycles summed over
     the 8 XCDs, so /8 / duration is the clock; SQ_VALU_MFMA_BUSY_CYCLES sums
     the busy cycles of every SIMD (32 per v_mfma_f32_32x32x16_bf16, 16 per
@@ -738,8 +742,9 @@ def busy_summary(csv_path, out, cmd):
              "ratios mean something only for dispatches of ~100 us and more: the counters of "
              "a short one also cover its launch and drain (hence clocks above the 2.4 GHz "
              "maximum).", "",
-             "| kernel | grid | launches | avg us | clock GHz | MFMA busy | L2 busy |",
-             "|---|---|---|---|---|---|---|"]
+             "| kernel | grid | launches | avg us | clock GHz | MFMA busy | L2 busy | "
+             "wait any | wait LDS issue | LDS conflict cycles |",
+             "|---|---|---|---|---|---|---|---|---|---|"]
     for (short, grid), d in sorted(per.items(), key=lambda kv: -sum(kv[1]["dur"].values())):
         ids = sorted(d["dur"])
         g = d["c"].get("GRBM_GUI_ACTIVE", {})
@@ -750,8 +755,17 @@ def busy_summary(csv_path, out, cmd):
         mf = sum(mb.get(i, 0.0) for i in ids) / len(ids)
         l2 = sum(tb.get(i, 0.0) for i in ids) / len(ids)
         clk = cyc / dur if dur else 0.0
+
+        def mean(c):
+            v = d["c"].get(c, {})
+            return sum(v.get(i, 0.0) for i in ids) / len(ids) if v else None
+
+        wc, wa, wl, bc = (mean(c) for c in ("SQ_WAVE_CYCLES", "SQ_WAIT_INST_ANY",
+                                            "SQ_WAIT_INST_LDS", "SQ_LDS_BANK_CONFLICT"))
+        frac = lambda a: f"{a / wc:.2f}" if a is not None and wc else "-"
         lines.append(f"| `{short}` | {grid} | {len(ids)} | {dur / 1e3:.1f} | {clk:.2f} | "
-                     f"{mf / (simds * cyc) if cyc else 0:.2f} | {l2 / cyc if cyc else 0:.2f} |")
+                     f"{mf / (simds * cyc) if cyc else 0:.2f} | {l2 / cyc if cyc else 0:.2f} | "
+                     f"{frac(wa)} | {frac(wl)} | {f'{bc:.3g}' if bc is not None else '-'} |")
     lines.append("")
     with open(out, "w") as f:
         f.write("\n".join(lines))
