@@ -641,7 +641,7 @@ def pmc_summary(fetch_csv, write_csv, cmd):
     for i, (name, grid, v) in fe.items():
         if "Cijk_" in name:
             short = "hipBLASLt " + name    # the same-tensor comparison leg
-        elif ("qgemm_kernel" not in name and "tall_dense_kernel" not in name and
+        elif ("qgemm_kernel" not in name and "tall_kernel" not in name and
                 "splitk_reduce" not in name and "dequant_kernel" not in name):
             continue
         else:
@@ -675,8 +675,10 @@ def pmc_summary(fetch_csv, write_csv, cmd):
             lines.append(f"| `{short}` | {grid} | {n} | {fb / n / 1e6:.1f} | {wb / n / 1e6:.1f} | "
                          f"up and down mixed (the same tensors as the dense GEMM) |")
             continue
-        tall_dense = "tall_dense_kernel" in short   # the 256 x 256 dense tile (tall.hip)
-        which = ffn_grid.get(grid) if "256, 256" in short or tall_dense else None
+        # the 256 x 256 tile of tall.hip: mode 0 dense bf16, 2 fused w8 dequant
+        tall_dense = "tall_kernel<0>" in short
+        tall_fused = "tall_kernel<2>" in short
+        which = ffn_grid.get(grid) if "256, 256" in short or tall_dense or tall_fused else None
         dense = ", 16, " in short or tall_dense
         a = (f"{alg(which, dense)[0] / 1e6:.1f} / {alg(which, dense)[1] / 1e6:.1f} ({which})"
              if which else "")
@@ -952,9 +954,10 @@ def main():
         "pct_bf16_peak": round(100 * ffn["tflops"] / PEAK_BF16_TFLOPS, 2),
         "ffn": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in ffn.items()},
         "roofline": {
-            "kernel": ("tall_dense_kernel (the 256x256 dense GEMM on 16x16x32 MFMAs, "
+            "kernel": ("tall_kernel<0> (the 256x256 dense bf16 GEMM on 16x16x32 MFMAs, "
                        "dequant-once route; up with GELU and down)" if ffn["route"] != "fused" else
-                       "qgemm_kernel<256,256,2,4,8,false> (up with GELU and down)"),
+                       "tall_kernel<2> (the 256x256 tile, w8 codes dequantized in registers; "
+                       "up with GELU and down)"),
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,

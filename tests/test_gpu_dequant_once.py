@@ -67,3 +67,51 @@ def test_dequant_once_declines_below_the_mma_floor(pkg):
         pkg.set_dequant_once(pkg.DEQUANT_ONCE_AUTO)
     assert pkg.dequant_once_takes(8160, 4096, 16384)   # AUTO: tall shapes
     assert not pkg.dequant_once_takes(320, 4096, 4096)
+
+
+TALL_CASES = [  # M, K, N, group, bias dtype, epilogue
+    (1000, 1152, 2056, 64, "f32", 1),   # ragged M, N % 256 != 0, GELU, 18 K steps
+    (520, 640, 1040, 32, "bf16", 0),    # group 32: two groups per 64-deep step
+    (300, 4096, 1024, 64, None, 1),
+    (300, 1024, 1030, 64, "f32", 0),    # N % 8 != 0: the template's 256 x 256 tile on both arms
+]
+
+
+@pytest.mark.parametrize("M,K,N,group,bias_kind,epi", TALL_CASES)
+def test_fused_tall_tile_is_bit_identical_to_dequant_once(pkg, M, K, N, group, bias_kind, epi):
+    """The 256 x 256 tile with w8 codes dequantized in registers once per workgroup
+    (dequant-once OFF) against the same tile over the bf16 expansion (ON): identical
+    bits, since both feed the MFMAs the same bf16 weights in the same K order; and the
+    oracle bar."""
+    rng = np.random.default_rng(M + 3 * N + group)
+    x = orc.bf16_rne(rng_normal(rng, (M, K)))
+    qw, codes, scales, biases, wb = make_qweight(pkg, rng_normal(rng, (N, K), 0.02), 8, group)
+    bias = rng_normal(rng, (N,), 0.01) if bias_kind else None
+    if bias_kind == "bf16":
+        bias = orc.bf16_to_f32(orc.bf16_rne(bias))
+        bd = dev_bf16(orc.bf16_rne(bias))
+    else:
+        bd = dev_f32(bias) if bias_kind else None
+    xd = dev_bf16(x)
+    outs = []
+    pkg.set_tile(pkg.TILE_TALL)
+    try:
+        for arm in (False, True):
+            pkg.set_dequant_once(arm)
+            route = pkg.linear_route(M, K, N, 8)
+            assert route["tile"] == pkg.TILE_TALL and route["dequant_once"] == int(arm)
+            say(f"tall tile M={M} K={K} N={N} w8g{group} bias={bias_kind} epi={epi} "
+                f"dequant_once={arm}")
+            y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+            pkg.linear_q(xd, qw, bd, y, M, K, N, epi)
+            torch.cuda.synchronize()
+            outs.append(host_bits(y))
+    finally:
+        pkg.set_dequant_once(pkg.DEQUANT_ONCE_AUTO)
+        pkg.set_tile(pkg.TILE_AUTO)
+    assert np.array_equal(outs[0], outs[1])
+    ref = orc.linear_f64(orc.bf16_to_f32(x), orc.bf16_to_f32(wb), bias)
+    if epi == 1:
+        ref = orc.gelu(ref)
+    got = orc.bf16_to_f32(outs[0])
+    assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) <= 1e-2
