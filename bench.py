@@ -151,7 +151,7 @@ def host_description():
 
 
 # ---- config 2: the FFN pair (headline) -------------------------------------------------
-def bench_ffn(pkg, torch, steps, warmup):
+def bench_ffn(pkg, torch, steps, warmup, same_tensors=True):
     """The pair through ltx25_linear_q with the library's default routing
     (the dequant-once arm at M = 8160: weight expansion + dense GEMM, both
     inside each timed call). The roofline kernel -- the dense GEMM the route
@@ -212,17 +212,18 @@ def bench_ffn(pkg, torch, steps, warmup):
     pkg.dequant(w2, d2, D, H)
     c1, c2 = pkg.dense_weight(d1), pkg.dense_weight(d2)
     h_pre = torch.empty_like(h)
-    ab = interleaved(torch, {
+    ab = {} if not same_tensors else interleaved(torch, {
         "ours_up_gelu": lambda: pkg.linear_qc(x, c1, None, h, M, D, H, pkg.EPI_GELU_TANH),
         "ours_up": lambda: pkg.linear_qc(x, c1, None, h_pre, M, D, H),
         "hipblaslt_up": lambda: torch.matmul(x, d1.t(), out=h_pre),
         "ours_down": lambda: pkg.linear_qc(h, c2, None, y, M, H, D),
         "hipblaslt_down": lambda: torch.matmul(h, d2.t(), out=y),
     }, rounds=max(10, steps))
-    out["same_tensors_vs_hipblaslt"] = {
-        k: {"best_us": v["best_ms"] * 1e3, "median_us": v["median_ms"] * 1e3,
-            "best_TFLOPs": flop / (v["best_ms"] * 1e-3) / 1e12}
-        for k, v in ab.items()}
+    if ab:
+        out["same_tensors_vs_hipblaslt"] = {
+            k: {"best_us": v["best_ms"] * 1e3, "median_us": v["median_ms"] * 1e3,
+                "best_TFLOPs": flop / (v["best_ms"] * 1e-3) / 1e12}
+            for k, v in ab.items()}
     if route == "fused":
         out["kernel_mean_ms"] = (up_ms + down_ms) / 2
         return out
@@ -612,6 +613,22 @@ def load_traffic():
     return None
 
 
+# The roofline kernel's launches by rocprofv3 (kernel trace of the FFN leg
+# without the same-tensor comparison, so every launch of the kernel at the
+# two FFN shapes is the route's own): written by --kernel-grid-summary,
+# read back into the bench line beside the HIP-event figure.
+ROOF_JSON = os.path.join(ROOT, "profiles", "roofline_kernel_stats.json")
+FFN_GRIDS = {((8160 + 255) // 256) * (16384 // 256) * 512: "up",
+             ((8160 + 255) // 256) * (4096 // 256) * 512: "down"}
+
+
+def load_roof():
+    if os.path.exists(ROOF_JSON):
+        with open(ROOF_JSON) as f:
+            return json.load(f)
+    return None
+
+
 def _pmc_rows(path):
     import csv
 
@@ -827,6 +844,21 @@ def kernel_grid_summary(trace_csv, out, cmd, note):
             continue
         lines.append(f"| `{name}` | {grid} | {len(v)} | {statistics.median(v):.1f} | "
                      f"{statistics.mean(v):.1f} | {min(v):.1f} |")
+    # the roofline kernel (tall_kernel<0> at the two FFN grids), when traced
+    ffn = {FFN_GRIDS[g]: statistics.mean(v) for (n, g), v in groups.items()
+           if "tall_kernel<0>" in n and g in FFN_GRIDS}
+    if len(ffn) == 2:
+        mean_us = (ffn["up"] + ffn["down"]) / 2
+        flop = 2.0 * 8160 * 4096 * 16384
+        tf = flop / (mean_us * 1e-6) / 1e12
+        lines += ["", f"Roofline kernel (`tall_kernel<0>`, mean of the up and down means): "
+                  f"{mean_us:.1f} us per launch = {tf:.1f} TFLOP/s = "
+                  f"{tf / PEAK_BF16_TFLOPS:.4f} of the bf16 peak."]
+        with open(ROOF_JSON, "w") as f:
+            json.dump({"up_us": round(ffn["up"], 2), "down_us": round(ffn["down"], 2),
+                       "mean_us": round(mean_us, 2), "tflops": round(tf, 2),
+                       "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                       "source": os.path.relpath(out, ROOT)}, f, indent=1)
     with open(out, "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
@@ -846,6 +878,9 @@ def main():
     ap.add_argument("--skip-audio", action="store_true")
     ap.add_argument("--skip-i8", action="store_true")
     ap.add_argument("--skip-c4", action="store_true")
+    ap.add_argument("--skip-hipblaslt", action="store_true",
+                    help="skip the FFN leg's same-tensor comparison with hipBLASLt (for a kernel "
+                         "trace whose launches of the roofline kernel are all the route's own)")
     ap.add_argument("--skip-next", action="store_true",
                     help="skip the LoRA-delta and dequant-once measurements")
     ap.add_argument("--profile-copy", action="store_true",
@@ -888,7 +923,7 @@ def main():
     pkg.check(pkg.load().ltx25_init())
 
     log(f"FFN pair (config 2): warmup {args.warmup}, steps {args.steps}")
-    ffn = bench_ffn(pkg, torch, args.steps, args.warmup)
+    ffn = bench_ffn(pkg, torch, args.steps, args.warmup, same_tensors=not args.skip_hipblaslt)
     log(f"  {ffn['tflops']:.1f} TFLOP/s, up {ffn['up_ms']:.3f} ms, down {ffn['down_ms']:.3f} ms")
     torch.cuda.empty_cache()
     extra = {}
@@ -935,6 +970,7 @@ def main():
 
     achieved = ffn["flop_per_launch"] / (ffn["kernel_mean_ms"] * 1e-3) / 1e12
     traffic = load_traffic()
+    roof = load_roof()
     line = {
         "metric": "qlinear TFLOP/s + % MFMA peak at M=8160 K=4096 N=16384 w8g64; audio GB/s",
         "value": round(ffn["tflops"], 2),
@@ -964,6 +1000,9 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": traffic.get("traffic_bytes") if traffic else None,
+            # the same kernel's mean launch time by rocprofv3 (committed profile)
+            "rocprof_mean_us": roof.get("mean_us") if roof else None,
+            "frac_rocprof": roof.get("frac") if roof else None,
         },
         "cpu_baseline": cpu,
     }
