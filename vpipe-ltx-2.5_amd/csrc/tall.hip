@@ -70,7 +70,9 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef int i32x4v __attribute__((ext_vector_type(4)));
 
 struct TallParams {
-  const void* x;           // bf16 [M][K] or int8 [M][K]
+  const void* x;           // bf16 [M][K] or int8 [M][K]; with x2: bf16 [M][kx]
+  const void* x2;          // the two-part activation's columns [kx, K), bf16 [M][K - kx]
+  int kx;                  // columns of x when x2 is set (a multiple of 64)
   const void* w;           // bf16 [N][K] or int8 [N][K]
   const void* bias;
   const float* sx;         // int8 mode: per-row activation scales
@@ -107,10 +109,11 @@ __device__ __forceinline__ void unroll(F&& f)
   unroll_seq(f, std::make_integer_sequence<int, N>{});
 }
 
-template <int MODE>
+template <int MODE, bool FOLD>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 tall_kernel(TallParams p)
 {
+  static_assert(!FOLD || MODE == 0, "the two-part activation is a bf16-mode operand");
   constexpr bool I8 = MODE == kModeI8;
   constexpr bool W8 = MODE == kModeW8;
   constexpr int kEB = I8 ? 1 : 2;   // bytes per X element
@@ -201,8 +204,28 @@ tall_kernel(TallParams p)
   const int dst = lr * kRow + lc * 8;
   uint4 xreg[kLd], wreg[kLd];
   // s: the step whose 128 bytes per row are loaded
+  // FOLD: the activation is [x | x2]; a step lies in one part, chosen by
+  // uniform selects (a branch would split the step's scheduling regions).
+  // The row offset is formed per load from the row and the part's row
+  // pitch, so the fold carries no second offset array.
+  const int fsteps = FOLD ? p.kx / kBK : 0;
+  const uint32_t rb1 = FOLD ? (uint32_t)p.kx * 2u : 0u;
+  const uint32_t rb2 = FOLD ? (uint32_t)(p.K - p.kx) * 2u : 0u;
+  const __amdgpu_buffer_rsrc_t xr1 = FOLD ? make_rsrc(p.x, (size_t)p.M * rb1) : xr;
+  const __amdgpu_buffer_rsrc_t xr2 = FOLD ? make_rsrc(p.x2, (size_t)p.M * rb2) : xr;
+  const uint32_t xrow = (uint32_t)(m0 + lr);
   auto load_x = [&](int s, int i) {
-    xreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff[i], s * kSB, 0));
+    if constexpr (FOLD) {
+      const bool second = s >= fsteps;
+      const uint32_t rb = second ? rb2 : rb1;
+      const int ss = second ? s - fsteps : s;
+      xreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              second ? xr2 : xr1,
+                                              (int)((xrow + 64u * i) * rb + (uint32_t)lc * 16u),
+                                              ss * kSB, 0));
+    } else {
+      xreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff[i], s * kSB, 0));
+    }
   };
   auto load_w = [&](int s, int i) {
     wreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woff[i], s * kSB, 0));
@@ -451,11 +474,15 @@ hipError_t launch_tall(const TallParams& p, int mode, hipStream_t stream)
 {
   const dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
   if (mode == kModeI8) {
-    hipLaunchKernelGGL(tall_kernel<kModeI8>, grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((tall_kernel<kModeI8, false>), grid, dim3(kThreads), 0, stream, p);
   } else if (mode == kModeW8) {
-    hipLaunchKernelGGL(tall_kernel<kModeW8>, grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((tall_kernel<kModeW8, false>), grid, dim3(kThreads), 0, stream, p);
   } else {
-    hipLaunchKernelGGL(tall_kernel<kModeBf16>, grid, dim3(kThreads), 0, stream, p);
+    if (p.x2 != nullptr) {
+      hipLaunchKernelGGL((tall_kernel<kModeBf16, true>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((tall_kernel<kModeBf16, false>), grid, dim3(kThreads), 0, stream, p);
+    }
   }
   return hipGetLastError();
 }
@@ -464,10 +491,11 @@ hipError_t launch_tall(const TallParams& p, int mode, hipStream_t stream)
 
 bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan)
 {
-  // The template keeps the two-part activation, the accumulating output and
-  // rows that are not whole 16-byte chunks. The per-lane byte offsets are
-  // 32-bit, rows past the last tile's end included.
-  return plan.tile == 0 && plan.splits == 1 && d.bits == 16 && d.x2 == nullptr &&
+  // The template keeps the accumulating output and rows that are not whole
+  // 16-byte chunks. The per-lane byte offsets are 32-bit, rows past the last
+  // tile's end included.
+  return plan.tile == 0 && plan.splits == 1 && d.bits == 16 &&
+         (d.x2 == nullptr || (d.kx > 0 && d.kx < d.K && d.kx % kBK == 0)) &&
          d.y_in == nullptr && d.N % 8 == 0 && d.K % kBK == 0 && d.K >= kBK &&
          (size_t)(d.M + kBM) * d.K * 2 < kFourGib && (size_t)(d.N + kBN) * d.K * 2 < kFourGib;
 }
@@ -511,11 +539,14 @@ hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream)
   }
   if (d.M < 1 || d.N < 8 || d.N % 8 != 0 || d.K < kBK || d.K % kBK != 0 || d.bits != 16 ||
       (size_t)d.M * d.K * 2 >= kTwoGib || (size_t)d.N * d.K * 2 >= kTwoGib ||
-      (size_t)d.M * d.N * 2 >= kTwoGib) {
+      (size_t)d.M * d.N * 2 >= kTwoGib ||
+      (d.x2 != nullptr && (d.kx <= 0 || d.kx >= d.K || d.kx % kBK != 0))) {
     return hipErrorInvalidValue;
   }
   TallParams p = {};
   p.x = d.x;
+  p.x2 = d.x2;
+  p.kx = d.x2 != nullptr ? d.kx : d.K;
   p.w = d.w;
   p.bias = d.bias;
   p.y = d.y;
