@@ -176,8 +176,10 @@ int ltx25_dequant(void* stream, const ltx25_qweight* w, void* out_bf16,
  * in-register dequant, so both routes return the same bits; they differ in
  * speed and in 2 B per weight of extra traffic. The fused kernel
  * dequantizes each weight once per 256-row tile, so the arm wins on tall
- * GEMMs: measured on MI355X at the DiT's widths it is 3-17% faster from
- * M = 4096 up and slower below M = 2048.
+ * GEMMs: measured on MI355X at the DiT's widths (4096 -> 4096 / 12288 /
+ * 16384, 16384 -> 4096) it is 2-22% faster from M = 1536 up, 4-12% faster
+ * at M = 1024 except for 4096 -> 16384 (8% slower there), and 5-13% slower
+ * at M = 512.
  *   OFF   always the fused dequant-in-GEMM kernel
  *   ON    the arm whenever the dense tile takes the shape (M >= 64,
  *         N >= 16: the reference's mma_eligible_ floor,
@@ -189,7 +191,7 @@ int ltx25_dequant(void* stream, const ltx25_qweight* w, void* out_bf16,
 #define LTX25_DEQUANT_ONCE_OFF 0
 #define LTX25_DEQUANT_ONCE_ON 1
 #define LTX25_DEQUANT_ONCE_AUTO 2
-#define LTX25_DEQUANT_ONCE_AUTO_MIN_M 4096
+#define LTX25_DEQUANT_ONCE_AUTO_MIN_M 1024
 int ltx25_set_dequant_once(int mode);
 
 /* 1 when ltx25_linear_q would take the dequant-once arm for this shape

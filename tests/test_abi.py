@@ -81,7 +81,8 @@ def test_dequant_once_and_lora_gates(pkg, lib):
     # AUTO by default: the arm for tall GEMMs only
     assert pkg.dequant_once_takes(8160, 4096, 16384)
     assert pkg.dequant_once_takes(4096, 2048, 8192)
-    assert not pkg.dequant_once_takes(4095, 4096, 4096)
+    assert pkg.dequant_once_takes(1024, 4096, 4096)
+    assert not pkg.dequant_once_takes(1023, 4096, 4096)
     assert not pkg.dequant_once_takes(126, 2048, 6144)
     try:
         pkg.set_dequant_once(pkg.DEQUANT_ONCE_OFF)

@@ -140,7 +140,7 @@ def test_fold_a_not_16_byte_aligned(pkg, dev):
 def test_no_fold_is_the_reference_sequence(pkg, dev, epi):
     """Below the dequant-once threshold (AUTO) the call is linear, lora_add,
     GELU: bit-identical to issuing them one by one."""
-    M, K, N, rank = 1024, 1024, 2048, 32
+    M, K, N, rank = 512, 1024, 2048, 32
     pkg.set_dequant_once(pkg.DEQUANT_ONCE_AUTO)
     assert not pkg.lora_fold_takes(M, K, N, rank, 8)
     xb, qw, wb, ab, bb, bias = _operands(pkg, M, K, N, rank, 8, 64, "f32", 11)
