@@ -1,11 +1,15 @@
-// The 256 x 256 GEMM tile on the 16-row MFMAs, in two operand modes:
+// The 256 x 256 GEMM tile on the 16-row MFMAs, in three operand modes:
 //   - bf16: y = x . w^T (+ bias) (+ GELU) on v_mfma_f32_16x16x32_bf16, for
 //     the dequant-once arm of the quantized linear (the weight expanded to
-//     bf16 once per call) and for dense weights. Same tile, operand feed and
-//     epilogue as the template in qgemm.hip, with 16x16x32 instead of
-//     32x32x16: with identical LDS traffic the 16x16x32 main loop runs ~10%
-//     faster on this GPU, and its sums come out bit-identical to the
-//     32x32x16 tile's (the fused-dequant route, which stays on the template);
+//     bf16 once per call), for dense weights, and for the LoRA fold's
+//     two-part activation [x | r]. Same tile, operand feed and epilogue as
+//     the template in qgemm.hip, with 16x16x32 instead of 32x32x16: with
+//     identical LDS traffic the 16x16x32 main loop runs ~10% faster on this
+//     GPU, and its sums come out bit-identical to the 32x32x16 tile's;
+//   - w8: the same tile with u8 codes (groups of 64 or 32) dequantized in
+//     registers once per workgroup before the LDS write, with the expansion
+//     kernel's arithmetic, so its results equal the bf16 mode's over the
+//     expansion bit for bit;
 //   - int8: the int8 tier's GEMM, int8 x int8 -> exact int32 on
 //     v_mfma_i32_16x16x64_i8, 128 of K per step in the same 128-byte row
 //     segments (so every fragment offset is the bf16 mode's), epilogue
