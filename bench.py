@@ -624,6 +624,7 @@ def load_traffic():
 # two FFN shapes is the route's own): written by --kernel-grid-summary,
 # read back into the bench line beside the HIP-event figure.
 ROOF_JSON = os.path.join(ROOT, "profiles", "roofline_kernel_stats.json")
+ROOF_MD = os.path.join(ROOT, "profiles", "roofline_kernel_stats.md")  # the one summary that writes it
 FFN_GRIDS = {((8160 + 255) // 256) * (16384 // 256) * 512: "up",
              ((8160 + 255) // 256) * (4096 // 256) * 512: "down"}
 
@@ -633,6 +634,15 @@ def load_roof():
         with open(ROOF_JSON) as f:
             return json.load(f)
     return None
+
+
+def tall_mode(name):
+    """The operand mode of a tall.hip launch (0 dense bf16, 1 int8, 2 fused w8) read from its
+    kernel name (`tall_kernel<0>` or `tall_kernel<0, false>`), else None."""
+    import re
+
+    m = re.search(r"tall_kernel<(\d)[,>]", name)
+    return int(m.group(1)) if m else None
 
 
 def _pmc_rows(path):
@@ -699,8 +709,8 @@ def pmc_summary(fetch_csv, write_csv, cmd):
                          f"up and down mixed (the same tensors as the dense GEMM) |")
             continue
         # the 256 x 256 tile of tall.hip: mode 0 dense bf16, 2 fused w8 dequant
-        tall_dense = "tall_kernel<0>" in short
-        tall_fused = "tall_kernel<2>" in short
+        tall_dense = tall_mode(short) == 0
+        tall_fused = tall_mode(short) == 2
         which = ffn_grid.get(grid) if "256, 256" in short or tall_dense or tall_fused else None
         dense = ", 16, " in short or tall_dense
         a = (f"{alg(which, dense)[0] / 1e6:.1f} / {alg(which, dense)[1] / 1e6:.1f} ({which})"
@@ -850,10 +860,11 @@ def kernel_grid_summary(trace_csv, out, cmd, note):
             continue
         lines.append(f"| `{name}` | {grid} | {len(v)} | {statistics.median(v):.1f} | "
                      f"{statistics.mean(v):.1f} | {min(v):.1f} |")
-    # the roofline kernel (tall_kernel<0> at the two FFN grids), when traced
+    # the roofline kernel (tall_kernel<0> at the two FFN grids), when traced for the roofline
+    # summary (other traces, e.g. the audio leg's, also hold FFN launches)
     ffn = {FFN_GRIDS[g]: statistics.mean(v) for (n, g), v in groups.items()
-           if "tall_kernel<0>" in n and g in FFN_GRIDS}
-    if len(ffn) == 2:
+           if tall_mode(n) == 0 and g in FFN_GRIDS}
+    if len(ffn) == 2 and os.path.basename(out) == os.path.basename(ROOF_MD):
         mean_us = (ffn["up"] + ffn["down"]) / 2
         flop = 2.0 * 8160 * 4096 * 16384
         tf = flop / (mean_us * 1e-6) / 1e12
