@@ -13,7 +13,7 @@ Also reported on the same line:
             achieved HBM GB/s of algorithmic bytes
   i8        config 3: the int8 GEMM at 8160x4096->{4096,16384} on
             pre-quantized operands, TOP/s
-  c4        config 4: the 28 linears of one joint audio-video block (22
+  c4        config 4: the 28 linears of one joint audio-video block (20
             launches with the fused QKV / KV packs) over 48 blocks of
             distinct weights, seconds of linear time per denoise step
   roofline  the dominant kernel: at M = 8160 linear_q's default route is the
@@ -36,6 +36,7 @@ import ctypes
 import importlib.util
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -542,10 +543,32 @@ def bench_c4(pkg, torch, steps, warmup, blocks=48):
         step()
     torch.cuda.synchronize()
     s = (time.perf_counter() - t0) / steps
+    # block 0's launches timed one at a time after the timed region (HIP events on the launch
+    # stream, median of 10 after 2), with the route each took: a badly routed shape shows here
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    per_launch = {}
+    for (name, _, _, _, _, _), (xa, M, K, N, qw, b, gelu) in zip(BLOCK, stack[0]):
+        ts = []
+        for r in range(12):
+            ev0.record()
+            pkg.linear_q(xa, qw, b, outs[(M, N)], M, K, N,
+                         pkg.EPI_GELU_TANH if gelu else pkg.EPI_NONE)
+            ev1.record()
+            torch.cuda.synchronize()
+            if r >= 2:
+                ts.append(ev0.elapsed_time(ev1) * 1e3)
+        us = statistics.median(ts)
+        route = pkg.linear_route(M, K, N, 8)
+        per_launch[name] = {"M": M, "K": K, "N": N, "us": round(us, 1),
+                            "tflops": round(2.0 * M * K * N / us / 1e6, 1),
+                            "tile": route["tile"], "dequant_once": route["dequant_once"],
+                            "splits": route["splits"]}
     return {"s_per_denoise_step": s, "tflops": flop_block * blocks / s / 1e12,
             "flop_per_block": flop_block, "params": params, "blocks": blocks,
             "launches_per_block": len(BLOCK), "timed_steps": steps, "warmup_steps": warmup,
-            "activations": "re-seeded per block (seeds 1000..1047)"}
+            "activations": "re-seeded per block (seeds 1000..1047)",
+            "block0_launches_us_sum": round(sum(v["us"] for v in per_launch.values()), 1),
+            "block0_per_launch": per_launch}
 
 
 # ---- CPU baseline -------------------------------------------------------------------------
