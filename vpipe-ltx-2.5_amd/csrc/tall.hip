@@ -130,6 +130,13 @@ tall_kernel(TallParams p)
   const int wn = wave & 3;
   int tm, tn;
   map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  // N-tiles relabelled tn -> 5 tn mod tiles_n (a bijection when 5 does not
+  // divide tiles_n). The tiles a round of workgroups finishes together then
+  // store scattered 512-byte segments of each output row, not two runs of
+  // four adjacent ones: 1.9% faster on the 8160 x 4096 -> 16384 GEMM, 0.5% on
+  // 16384 -> 4096 (interleaved best-of-24; a regular stride-8 interleave of
+  // the N-tiles measured no gain). The XCD grouping of the tiles is unchanged.
+  if (p.tiles_n % 5 != 0) { tn = (tn * 5) % p.tiles_n; }
   const int m0 = tm * kBM;
   const int n0 = tn * kBN;
   const uint32_t row_bytes = (uint32_t)p.K * kEB;
