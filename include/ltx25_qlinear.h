@@ -82,7 +82,27 @@ typedef struct ltx25_qweight {
 /* Select and check the device (the current HIP device must be gfx950) and
  * set up kernel attributes. Idempotent. Every compute entry point calls it
  * on first use.
- * Replaces MetalOps::init (src/ltx25-metal-ops.h:64). */
+ * Replaces MetalOps::init (src/ltx25-metal-ops.h:64).
+ *
+ * Route overrides from the environment, the reference's init-time A/B
+ * knobs (src/ltx25-metal-ops.cc:186-231; the i8 tier's VPIPE_I8_GEMM,
+ * src/ltx25-metal-ops.cc:749-757). Every call reads them, before the device
+ * check (so a host without a GPU can still plan routes), and applies the
+ * ones that are SET onto the process-wide switches below; an unset variable
+ * leaves its switch as it is:
+ *   VPIPE_LTX25_NO_MMA          dequant-once OFF and the int8 tier off: every
+ *                               quantized weight runs the fused
+ *                               dequant-in-GEMM kernel (the reference's qmm)
+ *   VPIPE_LTX25_NO_DEQUANT_MMA  dequant-once OFF
+ *   VPIPE_LTX25_MMA_MIN_M=v     v > 0: AUTO takes the dequant-once arm from
+ *                               M >= v (the reference's gate on that arm)
+ *   VPIPE_LTX25_MMA_TILE=t      128: LTX25_TILE_MID; 256 or 512:
+ *                               LTX25_TILE_TALL; other values ignored
+ *   VPIPE_LTX25_NO_LORA_MMA     LoRA route FUSED (no matrix-core pair)
+ *   VPIPE_I8_GEMM=0|1           the int8 tier off / on
+ * The reference keeps these per MetalOps instance; here they are
+ * process-wide, so a knob set around one ltx25_init stays in force until a
+ * setter or a later ltx25_init changes it. */
 int ltx25_init(void);
 
 /* Message for the last failure on this thread ("" when none). */
@@ -185,6 +205,7 @@ int ltx25_dequant(void* stream, const ltx25_qweight* w, void* out_bf16,
  *         N >= 16: the reference's mma_eligible_ floor,
  *         src/ltx25-metal-ops.cc:342-374)
  *   AUTO  (the default) the arm from M >= LTX25_DEQUANT_ONCE_AUTO_MIN_M
+ *         (or from VPIPE_LTX25_MMA_MIN_M when ltx25_init found it set)
  * The reference takes its dequant_mma_ route first whenever it is eligible
  * (src/ltx25-metal-ops.cc:467-502, tried at :544); AUTO keeps that route
  * where it is the faster one on this hardware. */

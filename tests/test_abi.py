@@ -6,6 +6,7 @@ import os
 import re
 import shutil
 import subprocess
+import sys
 
 import pytest
 import torch
@@ -306,3 +307,92 @@ def test_every_planned_split_fits_the_noalloc_scratch(pkg):
                 worst = max(worst, r["scratch_bytes"])
                 assert r["scratch_bytes"] <= cap, (M, K, N, r)
     assert worst > cap // 4        # the scan reaches plans near the cap
+
+
+_ENV_PROBE = r"""
+import ctypes, importlib.util, json, os, sys
+spec = importlib.util.spec_from_file_location("vpipe_ltx25_amd", sys.argv[1])
+pkg = importlib.util.module_from_spec(spec)
+sys.modules["vpipe_ltx25_amd"] = pkg
+spec.loader.exec_module(pkg)
+lib = pkg.load()
+before = pkg.linear_route(8160, 4096, 16384)
+rc = lib.ltx25_init()
+print(json.dumps({
+    "init_rc": rc,
+    "before": before,
+    "big": pkg.linear_route(8160, 4096, 16384),
+    "mid_m": pkg.dequant_once_takes(1000, 4096, 4096),
+    "i8": pkg.i8_takes(8160, 4096, 4096),
+    "lora": pkg.lora_on_matrix_cores(8160, 4096, 16384, 450),
+}))
+"""
+
+
+def _env_probe(env_extra):
+    env = {k: v for k, v in os.environ.items() if not k.startswith(("VPIPE_LTX25_", "VPIPE_I8"))}
+    env.update(env_extra)
+    out = subprocess.run([sys.executable, "-c", _ENV_PROBE,
+                          os.path.join(ROOT, "vpipe-ltx-2.5_amd", "__init__.py")],
+                         env=env, capture_output=True, text=True, timeout=120, check=True)
+    import json
+
+    return json.loads(out.stdout.strip().splitlines()[-1])
+
+
+def test_init_reads_the_reference_route_knobs():
+    """ltx25_init maps the reference's init-time A/B knobs
+    (src/ltx25-metal-ops.cc:186-231) and VPIPE_I8_GEMM onto the switches,
+    before the device check, so the routes change on any host."""
+    base = _env_probe({})
+    assert base["big"]["tile"] == 1 and base["big"]["dequant_once"] == 1
+    assert base["before"] == base["big"]
+    assert not base["mid_m"] and not base["i8"] and base["lora"]
+
+    r = _env_probe({"VPIPE_LTX25_NO_DEQUANT_MMA": "1"})
+    assert r["before"]["dequant_once"] == 1 and r["big"]["dequant_once"] == 0
+
+    r = _env_probe({"VPIPE_LTX25_MMA_TILE": "128"})
+    assert r["big"]["tile"] == 2
+    r = _env_probe({"VPIPE_LTX25_MMA_TILE": "512"})
+    assert r["big"]["tile"] == 1
+    r = _env_probe({"VPIPE_LTX25_MMA_TILE": "300"})     # not a reference tile: ignored
+    assert r["big"] == base["big"]
+
+    r = _env_probe({"VPIPE_LTX25_MMA_MIN_M": "900"})
+    assert r["mid_m"]
+    r = _env_probe({"VPIPE_LTX25_MMA_MIN_M": "-3"})
+    assert not r["mid_m"]
+
+    r = _env_probe({"VPIPE_I8_GEMM": "1"})
+    assert r["i8"] and r["big"]["i8"] == 1
+    r = _env_probe({"VPIPE_I8_GEMM": "1", "VPIPE_LTX25_NO_MMA": "1"})
+    assert not r["i8"] and r["big"]["dequant_once"] == 0 and r["big"]["i8"] == 0
+
+    r = _env_probe({"VPIPE_LTX25_NO_LORA_MMA": "1"})
+    assert not r["lora"]
+
+
+def test_fold_predicate_at_a_rank_wider_than_one_block(pkg):
+    """The fold's expansion writes the [W | B] tail in a loop over its
+    columns, so the predicate holds at any rank (2100 -> 2112 tail columns,
+    wider than one 256-thread block's 2048)."""
+    assert pkg.lora_fold_takes(1024, 256, 256, 2100, 8)
+    assert pkg.lora_fold_takes(8160, 4096, 16384, 2100, 8)
+    assert not pkg.lora_fold_takes(1023, 256, 256, 2100, 8)    # below the dequant-once arm
+
+
+def test_linear_q_lora_checks_epilogue_and_bias_first(pkg, lib):
+    """A bad epilogue or bias dtype is refused before either path touches
+    the device (the non-fold path would otherwise write y first)."""
+    import ctypes
+
+    fake = 0x1000
+    q = pkg.QWeightC(None, fake, fake, fake, 8, 64, 1)
+    for M in (64, 8160):     # the sequence, and the fold
+        assert lib.ltx25_linear_q_lora(None, fake, ctypes.byref(q), None, pkg.DT_NONE, fake, fake,
+                                       32, fake, M, 4096, 4096, 7) == pkg.E_INVAL
+        assert "epilogue" in pkg.last_error()
+        assert lib.ltx25_linear_q_lora(None, fake, ctypes.byref(q), fake, 9, fake, fake,
+                                       32, fake, M, 4096, 4096, 0) == pkg.E_INVAL
+        assert "bias" in pkg.last_error()

@@ -38,6 +38,9 @@ CASES = [
     ("rank 1", 192, 256, 256, 1, 8, 64, None, 0, "on"),
     ("256 x 256 tile at the dequant-once threshold", 4096, 1024, 8192, 32, 8, 64, "bf16", 1,
      "auto"),
+    # the expansion's [W | B] tail (2112 columns) is wider than one 256-thread
+    # block's 2048: written by the tail loop
+    ("rank 2100, tail wider than one block", 1024, 256, 256, 2100, 8, 64, "f32", 0, "auto"),
 ]
 MODES = {"on": 1, "auto": 2}
 

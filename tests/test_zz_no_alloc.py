@@ -31,6 +31,10 @@ PAIRS = [
      (4096, 4096, 4096, 8, 64, "bf16", 1), (300, 2048, 2048, 8, 64, "f32", 0)),
     ("w4 skinny split-K then w4 mid",
      (126, 4096, 4096, 4, 32, "f32", 0), (192, 2048, 1024, 4, 32, None, 0)),
+    # linear_q_ex expands the w4 weight and runs the 16x16x32 tile; the
+    # no-allocation call runs the template's fused 32x32x16 w4 tile
+    ("w4 tall (dequant-once in the entry point vs fused w4 tile) then w4 mid",
+     (1024, 4096, 4096, 4, 32, None, 1), (512, 1024, 2048, 4, 64, "f32", 0)),
 ]
 
 

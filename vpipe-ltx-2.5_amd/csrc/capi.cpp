@@ -16,6 +16,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -89,6 +90,7 @@ DeviceState g_dev[kMaxDevices];
 // process here), read on every call from any thread.
 std::atomic<int> g_i8_on{0};
 std::atomic<int> g_deq_once{LTX25_DEQUANT_ONCE_AUTO};
+std::atomic<int> g_deq_min_m{LTX25_DEQUANT_ONCE_AUTO_MIN_M};
 
 // Check (once per device) that the current device is gfx950.
 int current_device(DeviceState** out)
@@ -700,12 +702,45 @@ int run_fold(DeviceState* ds, hipStream_t st, const FoldPlan& f, const void* x,
   return LTX25_OK;
 }
 
+// The reference's init-time route knobs (src/ltx25-metal-ops.cc:186-231) and
+// the int8 tier's VPIPE_I8_GEMM, mapped onto this library's switches. Only
+// variables that are set change a switch.
+void apply_env_overrides()
+{
+  // the int8 tier sits under the matrix-core GEMM (src/ltx25-metal-ops.cc:
+  // 386-391), so VPIPE_LTX25_NO_MMA below overrides VPIPE_I8_GEMM=1
+  if (const char* e = std::getenv("VPIPE_I8_GEMM")) {
+    if (std::strcmp(e, "0") == 0) { g_i8_on.store(0, std::memory_order_relaxed); }
+    if (std::strcmp(e, "1") == 0) { g_i8_on.store(1, std::memory_order_relaxed); }
+  }
+  if (std::getenv("VPIPE_LTX25_NO_MMA") != nullptr) {
+    g_deq_once.store(LTX25_DEQUANT_ONCE_OFF, std::memory_order_relaxed);
+    g_i8_on.store(0, std::memory_order_relaxed);
+  }
+  if (std::getenv("VPIPE_LTX25_NO_DEQUANT_MMA") != nullptr) {
+    g_deq_once.store(LTX25_DEQUANT_ONCE_OFF, std::memory_order_relaxed);
+  }
+  if (const char* e = std::getenv("VPIPE_LTX25_MMA_MIN_M")) {
+    const int v = std::atoi(e);
+    if (v > 0) { g_deq_min_m.store(v, std::memory_order_relaxed); }
+  }
+  if (const char* e = std::getenv("VPIPE_LTX25_MMA_TILE")) {
+    const int v = std::atoi(e);
+    if (v == 128) { g_tile.store(LTX25_TILE_MID, std::memory_order_relaxed); }
+    if (v == 256 || v == 512) { g_tile.store(LTX25_TILE_TALL, std::memory_order_relaxed); }
+  }
+  if (std::getenv("VPIPE_LTX25_NO_LORA_MMA") != nullptr) {
+    g_lora_force.store(LTX25_LORA_FUSED, std::memory_order_relaxed);
+  }
+}
+
 }  // namespace
 
 extern "C" {
 
 int ltx25_init(void)
 {
+  apply_env_overrides();
   DeviceState* ds = nullptr;
   const int rc = current_device(&ds);
   if (rc != LTX25_OK) { return rc; }
@@ -846,7 +881,8 @@ int ltx25_dequant_once_takes(int M, int K, int N)
   const int mode = g_deq_once.load(std::memory_order_relaxed);
   if (mode == LTX25_DEQUANT_ONCE_OFF) { return 0; }
   if (M < 64 || N < 16 || K <= 0 || K % 64 != 0) { return 0; }
-  return mode == LTX25_DEQUANT_ONCE_ON || M >= LTX25_DEQUANT_ONCE_AUTO_MIN_M ? 1 : 0;
+  return mode == LTX25_DEQUANT_ONCE_ON || M >= g_deq_min_m.load(std::memory_order_relaxed) ? 1
+                                                                                           : 0;
 }
 
 int ltx25_lora_on_matrix_cores(int M, int K, int N, int rank)
@@ -979,6 +1015,15 @@ int ltx25_linear_q_lora(void* stream, const void* x, const ltx25_qweight* w, con
                         int K, int N, int epilogue)
 {
   hipStream_t st = (hipStream_t)stream;
+  // argument checks before any device work on either path (the fallback
+  // below writes y with the linear before it reaches its own epilogue)
+  if (epilogue != LTX25_EPI_NONE && epilogue != LTX25_EPI_GELU_TANH) {
+    return fail(LTX25_E_INVAL, "unknown epilogue %d", epilogue);
+  }
+  if (!bias_ok(bias, bias_dtype)) {
+    return fail(LTX25_E_INVAL, "bias dtype %d is not valid for a %s bias", bias_dtype,
+                bias == nullptr ? "null" : "non-null");
+  }
   if (rank > 0 && (a == nullptr || b == nullptr)) { return fail(LTX25_E_INVAL, "a or b is null"); }
   if (rank < 0) { return fail(LTX25_E_INVAL, "rank %d is negative", rank); }
   if (rank == 0 || M <= 0 || K <= 0 || N <= 0) {
@@ -995,13 +1040,6 @@ int ltx25_linear_q_lora(void* stream, const void* x, const ltx25_qweight* w, con
     if (x == nullptr || y == nullptr) { return fail(LTX25_E_INVAL, "x or y is null"); }
     int rc = check_qweight(w, K);
     if (rc != LTX25_OK) { return rc; }
-    if (!bias_ok(bias, bias_dtype)) {
-      return fail(LTX25_E_INVAL, "bias dtype %d is not valid for a %s bias", bias_dtype,
-                  bias == nullptr ? "null" : "non-null");
-    }
-    if (epilogue != LTX25_EPI_NONE && epilogue != LTX25_EPI_GELU_TANH) {
-      return fail(LTX25_E_INVAL, "unknown epilogue %d", epilogue);
-    }
     if ((rc = check_aligned("weight", w->codes)) != LTX25_OK) { return rc; }
     DeviceState* ds = nullptr;
     rc = current_device(&ds);
@@ -1020,7 +1058,6 @@ int ltx25_linear_q_lora(void* stream, const void* x, const ltx25_qweight* w, con
   rc = ltx25_lora_add(stream, x, a, b, y, nullptr, nullptr, M, K, N, rank);
   if (rc != LTX25_OK) { return rc; }
   if (epilogue == LTX25_EPI_GELU_TANH) { return ltx25_gelu_tanh(stream, y, y, (size_t)M * N); }
-  if (epilogue != LTX25_EPI_NONE) { return fail(LTX25_E_INVAL, "unknown epilogue %d", epilogue); }
   return LTX25_OK;
 }
 

@@ -140,8 +140,9 @@ bool plan_skinny(int M, int N, int K, int bits, int cu_count, GemmPlan& plan);
 hipError_t launch_skinny(const GemmDesc& d, const GemmPlan& plan, float* workspace,
                          hipStream_t stream);
 // The dense bf16 GEMM of the 256 x 256 tile on v_mfma_f32_16x16x32_bf16
-// (tall.hip): the dequant-once arm and dense weights, without a two-part
-// activation or y_in, N % 8 == 0. launch_gemm routes there when it takes.
+// (tall.hip): the dequant-once arm and dense weights, also with the LoRA
+// fold's two-part activation [x | r] (kx a multiple of 64); not y_in;
+// N % 8 == 0. launch_gemm routes there when it takes.
 bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan);
 // The same tile with w8 codes (groups of 64 or 32) dequantized in registers
 // once per workgroup before the LDS write: bit-identical to the dense tile

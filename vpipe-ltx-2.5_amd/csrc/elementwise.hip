@@ -116,9 +116,10 @@ dequant_kernel(const uint8_t* codes, const uint16_t* scales,
   const uint16_t* srow = scales + (size_t)n * gcols;
   const uint16_t* qrow = qbias + (size_t)n * gcols;
   uint16_t* orow = out + (size_t)n * ldo;
-  // columns [K, ldo) of the row: tail row n (tail_cols of it, zeros past them)
-  if (tail != nullptr && blockIdx.y == 0 && (int)threadIdx.x < (ldo - K) / 8) {
-    const int c = (int)threadIdx.x * 8;
+  // columns [K, ldo) of the row: tail row n (tail_cols of it, zeros past
+  // them), 8 columns per thread, strided by the block so any width is covered
+  for (int c = (int)threadIdx.x * 8; tail != nullptr && blockIdx.y == 0 && c < ldo - K;
+       c += kBlock * 8) {
     const uint16_t* trow = tail + (size_t)n * tail_ld;
     uint32_t w[4];
 #pragma unroll
@@ -310,7 +311,7 @@ hipError_t launch_dequant(const void* codes, const uint16_t* scales,
                           const uint16_t* tail, int tail_cols, int tail_ld)
 {
   if (ldo == 0) { ldo = K; }
-  if (ldo < K || ldo % 8 != 0 || (ldo - K) / 8 > kBlock ||
+  if (ldo < K || ldo % 8 != 0 ||
       (tail != nullptr && (tail_cols > ldo - K || tail_ld < tail_cols))) {
     return hipErrorInvalidValue;
   }

@@ -853,6 +853,9 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
       (plan.tile == 2 || d.bits != 16 || d.kx <= 0 || d.kx >= d.K || d.kx % kBK != 0)) {
     return hipErrorInvalidValue;   // the two-part activation: dense weights, MFMA tiles
   }
+  if (plan.tile == 2 && d.wn > 0 && d.wn < d.N) {
+    return hipErrorInvalidValue;   // the M <= 128 kernel reads all N weight rows
+  }
   if (plan.tile == 2) { return launch_skinny(d, plan, workspace, stream); }
   if (tall_dense_takes(d, plan) || tall_w8_takes(d, plan)) { return launch_tall_dense(d, stream); }
   KParams kp = {};
