@@ -661,9 +661,12 @@ def load_roof():
 
 def tall_mode(name):
     """The operand mode of a tall.hip launch (0 dense bf16, 1 int8, 2 fused w8) read from its
-    kernel name (`tall_kernel<0>` or `tall_kernel<0, false>`), else None."""
+    kernel name (`tall_kernel<0>` or `tall_kernel<0, false>`; the fused w8 tile is
+    `tall_w8_kernel`), else None."""
     import re
 
+    if "tall_w8_kernel" in name:
+        return 2
     m = re.search(r"tall_kernel<(\d)[,>]", name)
     return int(m.group(1)) if m else None
 
@@ -698,7 +701,8 @@ def pmc_summary(fetch_csv, write_csv, cmd):
         if "Cijk_" in name:
             short = "hipBLASLt " + name    # the same-tensor comparison leg
         elif ("qgemm_kernel" not in name and "tall_kernel" not in name and
-                "splitk_reduce" not in name and "dequant_kernel" not in name):
+                "tall_w8_kernel" not in name and "splitk_reduce" not in name and
+                "dequant_kernel" not in name):
             continue
         else:
             short = name[name.index("ltx25::"):].split("(ltx25")[0].replace("(anonymous namespace)::", "")

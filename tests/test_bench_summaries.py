@@ -26,6 +26,7 @@ def test_tall_mode_reads_both_name_forms(bench):
     assert bench.tall_mode("void ltx25::tall_kernel<0, false>") == 0
     assert bench.tall_mode("ltx25::tall_kernel<2, true>") == 2
     assert bench.tall_mode("ltx25::tall_kernel<1, false>") == 1
+    assert bench.tall_mode("void ltx25::(anonymous namespace)::tall_w8_kernel(ltx25::TallParams)") == 2
     assert bench.tall_mode("ltx25::dequant_kernel<8>") is None
     assert bench.tall_mode("ltx25::mid_kernel<0, false>") is None
 
