@@ -313,25 +313,11 @@ def bench_audio(pkg, torch, steps, warmup, sets=6):
     torch.cuda.synchronize()
     pass_ms = float(np.median([a.elapsed_time(b) for a, b in passes]))
     stream_ms = pass_ms / sets
-    # What a plain read of each GEMM's byte count reaches on this GPU (torch's sum over a
-    # float32 buffer of that size, distinct buffers rotated past the 256 MB memory-side
-    # cache): the launch-and-ramp ceiling for a 5-20 MB kernel, against which the 70%-of-
-    # HBM target for these GEMMs is set.
-    reads = {}
-    for name, K, N in AUDIO:
-        nbytes = gbytes(M, K, N)
-        bufs = [torch.empty((nbytes // 4,), dtype=torch.float32, device="cuda").normal_()
-                for _ in range(max(2, (300 << 20) // nbytes + 1))]
-        i = [0]
-
-        def rd(bufs=bufs, i=i):
-            bufs[i[0] % len(bufs)].sum()
-            i[0] += 1
-        r = interleaved(torch, {"read": rd}, rounds=max(20, steps * 2))["read"]
-        reads[name] = {"bytes": nbytes, "best_us": r["best_ms"] * 1e3,
-                       "best_GBps": nbytes / (r["best_ms"] * 1e-3) / 1e9,
-                       "median_GBps": nbytes / (r["median_ms"] * 1e-3) / 1e9}
-        del bufs
+    # The read ceiling for each GEMM's byte count: the library's own streaming-read probe
+    # (ltx25_probe_read: 16-byte loads, four in flight per lane, each workgroup on its own
+    # span), the best over grids of 256..2048 workgroups, its source rotated through a
+    # 384 MB pool so that the 256 MB memory-side cache cannot serve repeats.
+    reads = read_ceiling(pkg, torch, [(name, gbytes(M, K, N)) for name, K, N in AUDIO], steps)
     return {
         "GBps": gbs,
         "frac_hbm": gbs / PEAK_HBM_GBS,
@@ -344,6 +330,57 @@ def bench_audio(pkg, torch, steps, warmup, sets=6):
         "rotated_weight_MB": total_weight_mb,
         "plain_read_same_bytes": reads,
     }
+
+
+def read_ceiling(pkg, torch, sizes, steps):
+    """ltx25_probe_read at each (name, bytes): best and median time over interleaved rounds,
+    per grid size, and the grid that reads fastest."""
+    pool = torch.ones((384 << 20,), dtype=torch.uint8, device="cuda")
+    sink = torch.empty((65536,), dtype=torch.int32, device="cuda")
+    out = {}
+    for name, nbytes in sizes:
+        nbytes = (nbytes + 15) // 16 * 16
+        span = (nbytes + 4095) // 4096 * 4096
+        slots = (pool.numel() - span) // span
+        arms = {}
+        for blocks in (256, 512, 1024, 2048):
+            i = [0]
+
+            def rd(blocks=blocks, i=i):
+                off = (i[0] % slots) * span
+                pkg.probe_read(pool[off:], nbytes, sink, blocks)
+                i[0] += 1
+            arms[blocks] = rd
+        r = interleaved(torch, arms, rounds=max(20, steps * 2))
+        best = min(r, key=lambda b: r[b]["best_ms"])
+        out[name] = {"bytes": nbytes, "grid": best, "best_us": r[best]["best_ms"] * 1e3,
+                     "best_GBps": nbytes / (r[best]["best_ms"] * 1e-3) / 1e9,
+                     "median_GBps": nbytes / (r[best]["median_ms"] * 1e-3) / 1e9,
+                     "by_grid_best_us": {b: v["best_ms"] * 1e3 for b, v in r.items()}}
+    del pool
+    return out
+
+
+def bench_ceilings(pkg, torch, steps):
+    """The two ceilings the kernels are measured against, from the library's probes: the
+    streaming read at the four C1 GEMMs' and the FFN weight's byte counts, and the MFMA
+    stream (16x16x32 bf16, 16384 FLOP each) on zero and random operands at one and two waves
+    per SIMD."""
+    sizes = [(name, gbytes(126, K, N)) for name, K, N in AUDIO] + [("ffn_weight_codes",
+                                                                     16384 * 4096)]
+    reads = read_ceiling(pkg, torch, sizes, steps)
+    out = torch.empty((256,), dtype=torch.float32, device="cuda")
+    iters = 20000
+    mfma = {}
+    for random in (False, True):
+        for wps in (1, 2):
+            fn = lambda random=random, wps=wps: pkg.probe_mfma(iters, random, wps, out)
+            r = interleaved(torch, {"m": fn}, rounds=max(5, steps // 2))["m"]
+            flop = 256.0 * 4 * wps * 8 * iters * 16384
+            mfma[f"{'random' if random else 'zero'}_{wps}wave"] = {
+                "best_ms": r["best_ms"], "TFLOPs": flop / (r["best_ms"] * 1e-3) / 1e12,
+                "frac_bf16_peak": flop / (r["best_ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+    return {"read": reads, "mfma_stream": mfma}
 
 
 # ---- next rows: the LoRA delta and the dequant-once A/B arm ------------------------------
@@ -572,13 +609,22 @@ def bench_c4(pkg, torch, steps, warmup, blocks=48):
 
 
 # ---- CPU baseline -------------------------------------------------------------------------
-def cpu_baseline(rows=384):
-    """The reference's CPU linear (oracle/_ref: src/ltx25-block-ref.cc:11-28
-    compiled from the reference sources) on `rows` rows of the up-projection,
-    over the weight dequantized by the oracle's restatement of the
-    reference quantizer. Falls back to the oracle's restatement of the same
-    loop ("port") where oracle/_ref was not built."""
-    D, H = 4096, 16384
+def cpu_baseline(c2_rows=128, c3_rows=256):
+    """The CPU path on this host, per config, each
+    figure with its seconds and threads:
+      - c0, c1: the reference's CPU linear (oracle/_ref: src/ltx25-block-ref.cc:11-28
+        compiled from the reference sources; the oracle's restatement of the
+        same loop, "port", where oracle/_ref was not built) over the weight
+        dequantized by the oracle's restatement of the reference quantizer,
+        run fully: C0 320 x 4096 -> 4096 with an f32 bias, the four C1 audio
+        GEMMs at 126 tokens with bias (GB/s of the algorithmic bytes, the
+        metric config 1 is quoted in);
+      - c2: the same linear on a row sample of the up-projection 8160 x 4096
+        -> 16384 (the headline; the rate scales linearly with rows), and the
+        oracle's OpenMP f32 port on all threads;
+      - c3: the oracle's exact int32 GEMM (orc_i8_gemm_i32) on a row sample
+        of the int8 tier at 8160 x 4096 -> 4096.
+    The top-level value is the c2 rate (the headline's unit and workload)."""
     orc_path = os.path.join(ROOT, "oracle", "liboracle.so")
     ref_path = os.path.join(ROOT, "oracle", "_ref", "libltx25ref.so")
     if not os.path.exists(orc_path):
@@ -590,45 +636,99 @@ def cpu_baseline(rows=384):
     o.orc_dequant.argtypes = [vp, vp, vp, ci, ci, ci, ci, vp, vp]
     o.orc_linear_f64.argtypes = [vp, vp, vp, ci, ci, ci, vp]
     o.orc_linear_f32_omp.argtypes = [vp, vp, vp, ci, ci, ci, vp, ci]
-    w = np.empty((H, D), np.float32)
-    o.orc_fill_normal(w.ctypes.data, w.size, 7, 0.0, 0.02)
-    codes = np.empty((H, D // 4), np.uint32)
-    sc = np.empty((H, D // 64), np.uint16)
-    qb = np.empty((H, D // 64), np.uint16)
-    o.orc_quantize_affine(w.ctypes.data, H, D, 8, 64, codes.ctypes.data, sc.ctypes.data,
-                          qb.ctypes.data, None)
-    o.orc_dequant(codes.ctypes.data, sc.ctypes.data, qb.ctypes.data, H, D, 8, 64,
-                  w.ctypes.data, None)
-    x = np.empty((rows, D), np.float32)
-    o.orc_fill_normal(x.ctypes.data, x.size, 8, 0.0, 1.0)
-    out = np.empty((rows, H), np.float32)
+    o.orc_i8_gemm_i32.argtypes = [vp, vp, ci, ci, ci, vp]
     kind = "port"
-    fn = o.orc_linear_f64
+    lin = o.orc_linear_f64
     if os.path.exists(ref_path):
         r = ctypes.CDLL(ref_path)
         r.ref_linear.argtypes = [vp, vp, vp, ci, ci, ci, vp]
-        fn = r.ref_linear
+        lin = r.ref_linear
         kind = "reference"
-    t0 = time.perf_counter()
-    fn(x.ctypes.data, w.ctypes.data, None, rows, D, H, out.ctypes.data)
-    t = time.perf_counter() - t0
-    flop = 2.0 * rows * D * H
+
+    def normal(shape, seed, std):
+        a = np.empty(shape, np.float32)
+        o.orc_fill_normal(a.ctypes.data, a.size, seed, 0.0, std)
+        return a
+
+    def dequantized(N, K, seed):
+        """N(0, 0.02) weights through the reference quantizer, dequantized to f32."""
+        w = normal((N, K), seed, 0.02)
+        codes = np.empty((N, K // 4), np.uint32)
+        sc = np.empty((N, K // 64), np.uint16)
+        qb = np.empty((N, K // 64), np.uint16)
+        o.orc_quantize_affine(w.ctypes.data, N, K, 8, 64, codes.ctypes.data, sc.ctypes.data,
+                              qb.ctypes.data, None)
+        o.orc_dequant(codes.ctypes.data, sc.ctypes.data, qb.ctypes.data, N, K, 8, 64,
+                      w.ctypes.data, None)
+        return w
+
+    def timed_linear(M, K, N, seed, bias=True):
+        w = dequantized(N, K, seed)
+        x = normal((M, K), seed + 1, 1.0)
+        b = normal((N,), seed + 2, 0.01) if bias else None
+        out = np.empty((M, N), np.float32)
+        t0 = time.perf_counter()
+        lin(x.ctypes.data, w.ctypes.data, None if b is None else b.ctypes.data, M, K, N,
+            out.ctypes.data)
+        return time.perf_counter() - t0, x, w, out
+
+    host = host_description()
+    res = {"host": host, "kind": kind, "cores": 1}
+    # C0, fully
+    t, *_ = timed_linear(320, 4096, 4096, 11)
+    res["c0"] = {"value": 2.0 * 320 * 4096 * 4096 / t / 1e12, "unit": "TFLOP/s", "seconds": t,
+                 "cores": 1, "kind": kind,
+                 "sample": "all of config 0: 320 x 4096 -> 4096 w8g64 (dequantized to f32) + f32 "
+                           "bias, double accumulator, 1 thread"}
+    # C1, fully
+    t1 = 0.0
+    per = {}
+    for i, (name, K, N) in enumerate(AUDIO):
+        t, *_ = timed_linear(126, K, N, 21 + 3 * i)
+        per[name] = {"seconds": t, "GBps": gbytes(126, K, N) / t / 1e9}
+        t1 += t
+    c1_bytes = sum(gbytes(126, K, N) for _, K, N in AUDIO)
+    res["c1"] = {"value": c1_bytes / t1 / 1e9, "unit": "GB/s", "seconds": t1, "cores": 1,
+                 "kind": kind, "per_gemm": per,
+                 "sample": "all four config-1 audio GEMMs at 126 tokens with bias, back to "
+                           "back, double accumulator, 1 thread"}
+    # C2, row sample of the up-projection
+    D, H = 4096, 16384
+    t, x, w, out = timed_linear(c2_rows, D, H, 7, bias=False)
+    flop = 2.0 * c2_rows * D * H
     threads = min(16, os.cpu_count() or 1)
-    t1 = time.perf_counter()
-    o.orc_linear_f32_omp(x.ctypes.data, w.ctypes.data, None, rows, D, H, out.ctypes.data, threads)
-    t_omp = time.perf_counter() - t1
-    return {
-        "value": flop / t / 1e12,
+    t_omp0 = time.perf_counter()
+    o.orc_linear_f32_omp(x.ctypes.data, w.ctypes.data, None, c2_rows, D, H, out.ctypes.data,
+                         threads)
+    t_omp = time.perf_counter() - t_omp0
+    res["c2"] = {"value": flop / t / 1e12, "unit": "TFLOP/s", "seconds": t, "cores": 1,
+                 "kind": kind,
+                 "sample": (f"{c2_rows} of 8160 rows of the config-2 up-projection 4096->16384 "
+                            f"(w8g64 dequantized to f32), double accumulator, 1 thread; the rate "
+                            f"scales linearly to all rows"),
+                 "omp_f32": {"value": flop / t_omp / 1e12, "unit": "TFLOP/s", "cores": threads,
+                             "kind": "port", "seconds": t_omp}}
+    del x, w, out
+    # C3, row sample of the int8 GEMM (exact int32)
+    K3, N3 = 4096, 4096
+    rng = np.random.default_rng(31)
+    xq = rng.integers(-127, 128, size=(c3_rows, K3), dtype=np.int8)
+    wq = rng.integers(-127, 128, size=(N3, K3), dtype=np.int8)
+    acc = np.empty((c3_rows, N3), np.int32)
+    t0 = time.perf_counter()
+    o.orc_i8_gemm_i32(xq.ctypes.data, wq.ctypes.data, c3_rows, K3, N3, acc.ctypes.data)
+    t3 = time.perf_counter() - t0
+    res["c3"] = {"value": 2.0 * c3_rows * K3 * N3 / t3 / 1e12, "unit": "TOP/s", "seconds": t3,
+                 "cores": 1, "kind": "port",
+                 "sample": f"{c3_rows} of 8160 rows of the config-3 int8 GEMM 4096->4096, exact "
+                           f"int32 accumulation (the oracle's loop), 1 thread"}
+    res.update({
+        "value": res["c2"]["value"],
         "unit": "TFLOP/s",
-        "cores": 1,
-        "host": host_description(),
-        "kind": kind,
-        "sample": (f"{rows} of 8160 rows of the config-2 up-projection 4096->16384 (w8g64 "
-                   f"dequantized to f32), double accumulator, 1 thread, {t:.2f} s; "
-                   f"rate scales linearly to all rows"),
-        "omp_f32": {"value": flop / t_omp / 1e12, "unit": "TFLOP/s", "cores": threads,
-                    "kind": "port", "seconds": t_omp},
-    }
+        "sample": res["c2"]["sample"] + " (per-config figures under c0..c3)",
+        "omp_f32": res["c2"]["omp_f32"],
+    })
+    return res
 
 
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "qgemm_ffn_hbm_traffic.json")
@@ -927,6 +1027,11 @@ def main():
                          "trace whose launches of the roofline kernel are all the route's own)")
     ap.add_argument("--skip-next", action="store_true",
                     help="skip the LoRA-delta and dequant-once measurements")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="also measure the library's ceiling probes (streaming read at the audio "
+                         "GEMMs' byte counts, MFMA stream on zero and random operands)")
+    ap.add_argument("--ceilings-only", action="store_true",
+                    help="measure only the ceiling probes and print them as one JSON line")
     ap.add_argument("--profile-copy", action="store_true",
                     help="also run one plain 256 MiB device copy, the known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -966,6 +1071,9 @@ def main():
     torch.cuda.set_device(0)
     pkg.check(pkg.load().ltx25_init())
 
+    if args.ceilings_only:
+        print(json.dumps({"ceilings": bench_ceilings(pkg, torch, args.steps)}), flush=True)
+        return
     log(f"FFN pair (config 2): warmup {args.warmup}, steps {args.steps}")
     ffn = bench_ffn(pkg, torch, args.steps, args.warmup, same_tensors=not args.skip_hipblaslt)
     log(f"  {ffn['tflops']:.1f} TFLOP/s, up {ffn['up_ms']:.3f} ms, down {ffn['down_ms']:.3f} ms")
@@ -992,6 +1100,10 @@ def main():
         extra["ab_interleaved"] = bench_dequant_once(pkg, torch, max(5, args.steps // 2),
                                                      args.warmup)
         log(f"  {extra['lora']}\n  {extra['ab_interleaved']}")
+        torch.cuda.empty_cache()
+    if args.ceilings:
+        log("ceiling probes")
+        extra["ceilings"] = bench_ceilings(pkg, torch, args.steps)
         torch.cuda.empty_cache()
     if not args.skip_c4:
         log("48-block linear set (config 4)")

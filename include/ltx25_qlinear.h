@@ -462,6 +462,26 @@ int ltx25_pack_bind_qlinear(ltx25_pack* pack, void* stream, const char* name,
  * selection of src/ltx25-quant-family.cc:44-71. */
 int ltx25_pack_quantizable(const char* name, const char* dtype, int ndim);
 
+/* ---- measurement probes -------------------------------------------------- */
+
+/* No counterpart in the reference: the two ceilings this library's kernels
+ * are measured against (bench.py --ceilings), shipped so that the figures
+ * quoted beside the GEMMs can be reproduced from the library itself.
+ *
+ * Streaming read: `bytes` of device memory from `src` read once with
+ * 16-byte loads by `blocks` workgroups of 256 threads, each on its own
+ * contiguous span; one u32 per workgroup to `sink` (device, `blocks`
+ * words). src 16-byte aligned, bytes a positive multiple of 16, blocks in
+ * 1..65535. */
+int ltx25_probe_read(void* stream, const void* src, size_t bytes, void* sink, int blocks);
+
+/* MFMA stream: 256 workgroups of 1 or 2 waves per SIMD (`waves_per_simd`)
+ * each issue 8 x `iters` independent v_mfma_f32_16x16x32_bf16 (16384 FLOP
+ * each) on register operands, zero (`random` 0) or random bf16 of
+ * magnitude ~1 (`random` 1). `out` (device, 256 floats) is written only in
+ * the practically impossible case that a sum equals 1.2345. iters > 0. */
+int ltx25_probe_mfma(void* stream, int iters, int random, int waves_per_simd, void* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -102,6 +102,8 @@ SIGNATURES = {
     "ltx25_bias_add": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "ltx25_gelu_tanh": (_i, [_vp, _vp, _vp, _sz]),
     "ltx25_gate_heads": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "ltx25_probe_read": (_i, [_vp, _vp, _sz, _vp, _i]),
+    "ltx25_probe_mfma": (_i, [_vp, _i, _i, _i, _vp]),
     "ltx25_dequant": (_i, [_vp, ctypes.POINTER(QWeightC), _vp, _i, _i]),
     "ltx25_set_dequant_once": (_i, [_i]),
     "ltx25_dequant_once_takes": (_i, [_i, _i, _i]),
@@ -262,6 +264,17 @@ def gelu_tanh(x, y, stream=None) -> None:
 def gate_heads(y, logits, heads: int, tokens: int, head_dim: int, stream=None) -> None:
     check(load().ltx25_gate_heads(_stream(stream), _ptr(y), _ptr(logits), heads, tokens,
                                   head_dim))
+
+
+def probe_read(src, nbytes: int, sink, blocks: int, stream=None) -> None:
+    """The streaming-read ceiling probe (ltx25_probe_read)."""
+    check(load().ltx25_probe_read(_stream(stream), _ptr(src), nbytes, _ptr(sink), blocks))
+
+
+def probe_mfma(iters: int, random: bool, waves_per_simd: int, out, stream=None) -> None:
+    """The MFMA-stream ceiling probe (ltx25_probe_mfma)."""
+    check(load().ltx25_probe_mfma(_stream(stream), iters, 1 if random else 0, waves_per_simd,
+                                  _ptr(out)))
 
 
 def dequant(w: QWeight, out, N: int, K: int, stream=None) -> None:

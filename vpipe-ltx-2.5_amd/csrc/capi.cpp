@@ -1061,6 +1061,37 @@ int ltx25_linear_q_lora(void* stream, const void* x, const ltx25_qweight* w, con
   return LTX25_OK;
 }
 
+int ltx25_probe_read(void* stream, const void* src, size_t bytes, void* sink, int blocks)
+{
+  if (src == nullptr || sink == nullptr) { return fail(LTX25_E_INVAL, "src or sink is null"); }
+  if (bytes == 0 || bytes % 16 != 0 || !aligned16(src)) {
+    return fail(LTX25_E_INVAL, "bytes=%zu must be a positive multiple of 16 from a 16-byte "
+                "aligned src", bytes);
+  }
+  if (blocks < 1 || blocks > 65535) { return fail(LTX25_E_INVAL, "blocks=%d is not in 1..65535", blocks); }
+  DeviceState* ds = nullptr;
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_probe_read(src, bytes, (uint32_t*)sink, blocks,
+                                                (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "probe read launch");
+}
+
+int ltx25_probe_mfma(void* stream, int iters, int random, int waves_per_simd, void* out)
+{
+  if (out == nullptr) { return fail(LTX25_E_INVAL, "out is null"); }
+  if (iters < 1 || (random != 0 && random != 1) || (waves_per_simd != 1 && waves_per_simd != 2)) {
+    return fail(LTX25_E_INVAL, "iters=%d random=%d waves_per_simd=%d: iters > 0, random 0 or 1, "
+                "waves_per_simd 1 or 2", iters, random, waves_per_simd);
+  }
+  DeviceState* ds = nullptr;
+  const int rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_probe_mfma(iters, random, waves_per_simd, (float*)out,
+                                                (hipStream_t)stream);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "probe mfma launch");
+}
+
 int ltx25_set_i8_gemm(int on)
 {
   g_i8_on.store(on != 0 ? 1 : 0, std::memory_order_relaxed);

@@ -227,4 +227,13 @@ hipError_t launch_i8_gemm(const int8_t* xq, const float* sx,
                           int bias_type, int epilogue, uint16_t* y, int32_t* acc,
                           int M, int K, int N, hipStream_t stream);
 
+// Measurement probes (probes.hip): a streaming read of `bytes` (16-byte
+// aligned, a multiple of 16) over `blocks` workgroups, one word per
+// workgroup to `sink`; a stream of independent 16x16x32 bf16 MFMAs on zero
+// or random register operands, 256 workgroups of 1 or 2 waves per SIMD.
+hipError_t launch_probe_read(const void* src, size_t bytes, uint32_t* sink, int blocks,
+                             hipStream_t stream);
+hipError_t launch_probe_mfma(int iters, int random, int waves_per_simd, float* out,
+                             hipStream_t stream);
+
 }  // namespace ltx25
