@@ -396,48 +396,56 @@ def bench_lora(pkg, torch, steps, warmup):
     for rank in (32, 450):
         a = (torch.randn((rank, K), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
         b = (torch.randn((N, rank), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
-        fn = lambda: pkg.lora_add(x, a, b, y, M, K, N, rank)   # noqa: E731
-        for _ in range(warmup):
-            fn()
+        # the reference's signature passes r ([M][rank]) as caller scratch; the r-first
+        # route (rank 32 here) computes r into it
+        r = torch.empty((M, rank), dtype=torch.bfloat16, device="cuda")
+        arms = {"lora": lambda: pkg.lora_add(x, a, b, y, M, K, N, rank),   # noqa: E731
+                "lora_caller_r": lambda: pkg.lora_add(x, a, b, y, M, K, N, rank, r=r)}   # noqa: E731
+        for fn in arms.values():
+            for _ in range(warmup):
+                fn()
         timer = EventTimer(torch)
         for _ in range(steps):
-            timer.record("lora", fn)
+            for name, fn in arms.items():
+                timer.record(name, fn)
         torch.cuda.synchronize()
         ms = timer.mean_ms("lora")
         byt = M * K * 2 + rank * K * 2 + N * rank * 2 + 2 * M * N * 2
         flop = 2.0 * M * rank * (K + N)
-        out[f"rank{rank}"] = {"us": ms * 1e3, "GBps": byt / (ms * 1e-3) / 1e9,
+        out[f"rank{rank}"] = {"route": pkg.lora_route(x, a, b, y, M, K, N, rank),
+                              "us": ms * 1e3, "caller_r_us": timer.mean_ms("lora_caller_r") * 1e3,
+                              "GBps": byt / (ms * 1e-3) / 1e9,
                               "TFLOPs": flop / (ms * 1e-3) / 1e12,
                               "frac_of_linear": None}
-    # The adapter on the linear it rides on (the FFN up-projection with GELU, rank 32):
-    # the linear alone, the linear with the adapter folded into its GEMM
+    # The adapter on the linear it rides on (the FFN up-projection with GELU, ranks 32 and
+    # 450): the linear alone, the linear with the adapter folded into its GEMM
     # (ltx25_linear_q_lora), and the reference's sequence (linear, lora_add, GELU),
     # interleaved best-of-N.
     w = make_qweight(pkg, torch, N, K, g)
     h = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    rank = 32
-    a = (torch.randn((rank, K), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
-    b = (torch.randn((N, rank), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    for rank in (32, 450):
+        a = (torch.randn((rank, K), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        b = (torch.randn((N, rank), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
 
-    def seq():
-        pkg.linear_q(x, w, None, h, M, K, N)
-        pkg.lora_add(x, a, b, h, M, K, N, rank)
-        pkg.gelu_tanh(h, h)
-    ab = interleaved(torch, {
-        "linear": lambda: pkg.linear_q(x, w, None, h, M, K, N, pkg.EPI_GELU_TANH),
-        "fold": lambda: pkg.linear_q_lora(x, w, None, a, b, rank, h, M, K, N,
-                                          pkg.EPI_GELU_TANH),
-        "sequence": seq,
-    }, rounds=max(10, steps))
-    lin = ab["linear"]["best_ms"]
-    out["rank32_with_linear"] = {
-        "fold_taken": pkg.lora_fold_takes(M, K, N, rank, 8),
-        "linear_us": lin * 1e3,
-        "fold_us": ab["fold"]["best_ms"] * 1e3,
-        "sequence_us": ab["sequence"]["best_ms"] * 1e3,
-        "fold_overhead_frac": ab["fold"]["best_ms"] / lin - 1.0,
-        "sequence_overhead_frac": ab["sequence"]["best_ms"] / lin - 1.0,
-    }
+        def seq(a=a, b=b, rank=rank):
+            pkg.linear_q(x, w, None, h, M, K, N)
+            pkg.lora_add(x, a, b, h, M, K, N, rank)
+            pkg.gelu_tanh(h, h)
+        ab = interleaved(torch, {
+            "linear": lambda: pkg.linear_q(x, w, None, h, M, K, N, pkg.EPI_GELU_TANH),
+            "fold": lambda a=a, b=b, rank=rank: pkg.linear_q_lora(x, w, None, a, b, rank, h, M, K,
+                                                                  N, pkg.EPI_GELU_TANH),
+            "sequence": seq,
+        }, rounds=max(10, steps))
+        lin = ab["linear"]["best_ms"]
+        out[f"rank{rank}_with_linear"] = {
+            "fold_taken": pkg.lora_fold_takes(M, K, N, rank, 8),
+            "linear_us": lin * 1e3,
+            "fold_us": ab["fold"]["best_ms"] * 1e3,
+            "sequence_us": ab["sequence"]["best_ms"] * 1e3,
+            "fold_overhead_frac": ab["fold"]["best_ms"] / lin - 1.0,
+            "sequence_overhead_frac": ab["sequence"]["best_ms"] / lin - 1.0,
+        }
     return out
 
 

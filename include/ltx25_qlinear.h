@@ -228,8 +228,8 @@ int ltx25_dequant_once_takes(int M, int K, int N);
  *           CUs once, f32 partials summed in split order by a second launch
  *   SKINNY  at most 128 tokens: 32-column slices, K split between the 8
  *           waves (and across workgroups above K = 2048)
- * ltx25_set_tile forces one for every later linear (AUTO restores the
- * planner); a forced SKINNY falls back to the planner for shapes it cannot
+ * ltx25_set_tile forces one for every later linear and for the second GEMM
+ * of the LoRA pair (AUTO restores the planner); a forced SKINNY falls back to the planner for shapes it cannot
  * take (M > 128). Results are deterministic for a given route; different
  * routes sum in different orders. Process-wide, like the reference's
  * VPIPE_LTX25_MMA_TILE override (src/ltx25-metal-ops.cc:193-231, read at
@@ -268,8 +268,9 @@ int ltx25_linear_route(int M, int K, int N, int bits, ltx25_route* out);
  * - rank >= 96, M >= 256, K % 64 == 0, N % 8 == 0, 16-byte aligned x and y:
  *   the reference's matrix-core pair -- r on the dense GEMM, then the dense
  *   GEMM again with its accumulators seeded from y; the rank is padded to a
- *   multiple of 64 (a and b copied with zero rows / columns when needed) in
- *   a grow-only scratch that also holds r;
+ *   multiple of 64 (a's missing rows read as zeros; b copied with zero
+ *   columns when needed, and a when it is not 16-byte aligned) in a
+ *   grow-only scratch that also holds r;
  * - rank < 96 with M >= 512, K % 64 == 0, rank % 8 == 0 and the vector
  *   path's conditions (below): r on the dense GEMM into that scratch, then
  *   the fused kernel's y pass reading it;
@@ -277,8 +278,11 @@ int ltx25_linear_route(int M, int K, int N, int bits, ltx25_route* out);
  *   a and y with K % 8 == 0 and N % 8 == 0 take its vector path; when the
  *   rank is not a multiple of 8, b is first copied with its rows
  *   zero-padded to one).
- * `r` ([M][rank]) and `d` ([M][N]) are the reference signature's caller
- * scratch and are neither read nor written (either may be NULL). An empty
+ * `r` ([M][rank] bf16) and `d` ([M][N]) are the reference signature's
+ * caller scratch; either may be NULL. A 16-byte aligned `r` receives
+ * r = bf16(x . a^T) on the r-first route, and on the pair when rank is a
+ * multiple of 64, in place of the library's scratch; other routes leave it
+ * untouched. `d` is neither read nor written. An empty
  * shape (any of M, K, N, rank <= 0) is a no-op, as in the reference.
  * Pointers need only bf16 (2-byte) alignment.
  * Replaces MetalOps::lora_add (src/ltx25-metal-ops.h:107-133;

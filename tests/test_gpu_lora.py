@@ -162,3 +162,34 @@ def test_lora_is_deterministic(pkg, dev):
         torch.cuda.synchronize()
         outs.append(host_bits(yd))
     assert np.array_equal(outs[0], outs[1])
+
+
+# the reference's caller scratch r ([M][rank]): the r-first route, and the GEMM pair at a
+# rank that is a multiple of 64, compute r into it instead of the library's scratch
+CALLER_R = [("r first: rank 40, ragged M", 777, 1024, 2048, 40, RF),
+            ("GEMM pair, rank 128, no padding", 300, 2048, 1024, 128, P)]
+
+
+@pytest.mark.parametrize("what,M,K,N,rank,route", CALLER_R, ids=[s[0] for s in CALLER_R])
+def test_lora_caller_r_holds_r(pkg, dev, what, M, K, N, rank, route):
+    say(f"lora_add with the caller's r: {what}: M={M} K={K} N={N} rank={rank}")
+    x, a, b, y0 = draws(what, M, K, N, rank)
+    xb, ab, bb, yb = (orc.bf16_rne(t) for t in (x, a, b, y0))
+    xd, ad, bd = (dev_bf16(t) for t in (xb, ab, bb))
+    assert pkg.lora_route(xd, ad, bd, dev_bf16(yb), M, K, N, rank) == ROUTE[route]
+    # the library's scratch, then the caller's r (NaN-filled first): same kernels, same bits
+    y_lib = dev_bf16(yb)
+    pkg.lora_add(xd, ad, bd, y_lib, M, K, N, rank)
+    r = torch.full((M, rank), float("nan"), dtype=torch.bfloat16, device="cuda")
+    y_r = dev_bf16(yb)
+    pkg.lora_add(xd, ad, bd, y_r, M, K, N, rank, r=r)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(y_r), host_bits(y_lib))
+    got = orc.bf16_to_f32(host_bits(y_r))
+    ref = orc.bf16_to_f32(orc.lora_add(xb, ab, bb, yb))
+    assert max_rel(got, ref) <= MAX_REL
+    # r = bf16(x . a^T) landed in the caller's buffer
+    r_got = orc.bf16_to_f32(host_bits(r))
+    r_ref = orc.bf16_to_f32(xb).astype(np.float64) @ orc.bf16_to_f32(ab).astype(np.float64).T
+    assert np.isfinite(r_got).all()
+    assert max_rel(r_got, r_ref) <= MAX_REL

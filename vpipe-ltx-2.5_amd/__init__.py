@@ -311,7 +311,9 @@ def dequant_once_takes(M: int, K: int, N: int) -> bool:
 
 def lora_add(x, a, b, y, M: int, K: int, N: int, rank: int, r=None, d=None,
              stream=None) -> None:
-    """y += (x . a^T) . b^T in place (MetalOps::lora_add); r and d are unused scratch."""
+    """y += (x . a^T) . b^T in place (MetalOps::lora_add). r: optional caller scratch
+    [M][rank] (16-byte aligned) that receives r = bf16(x . a^T) on the r-first route and
+    on the GEMM pair when rank % 64 == 0; d is unused."""
     check(load().ltx25_lora_add(_stream(stream), _ptr(x), _ptr(a), _ptr(b), _ptr(y), _ptr(r),
                                 _ptr(d), M, K, N, rank))
 

@@ -513,22 +513,29 @@ int lora_route(int M, int K, int N, int rank, const void* x, const void* a, cons
 }
 
 int lora_pair(DeviceState* ds, hipStream_t st, const void* x, const void* a, const void* b,
-              void* y, int M, int K, int N, int rank)
+              void* y, void* r_caller, int M, int K, int N, int rank)
 {
   const int rk = (rank + 63) & ~63;
-  const bool pad_a = rk != rank || !aligned16(a);
+  // A's rows past `rank` read as zeros (the GEMM's weight-row bound), so A
+  // is copied only when it is not 16-byte aligned or the r GEMM plans the
+  // M <= 128 kernel, which takes whole weights only; B gets zero columns up
+  // to rk. The caller's r ([M][rank]) holds r when it has rk columns.
+  const ltx25::GemmPlan r_plan = ltx25::plan_gemm(M, rk, K, 16, ds->cu_count);
+  const bool pad_a = !aligned16(a) || (rk != rank && r_plan.tile == 2);
   const bool pad_b = rk != rank || !aligned16(b);
+  const bool own_r = r_caller == nullptr || rk != rank || !aligned16(r_caller);
   const size_t a_bytes = pad_a ? align256((size_t)rk * K * 2) : 0;
-  const size_t r_bytes = align256((size_t)M * rk * 2);
+  const size_t r_bytes = own_r ? align256((size_t)M * rk * 2) : 0;
   const size_t b_bytes = pad_b ? align256((size_t)N * rk * 2) : 0;
-  {
+  char* base = nullptr;
+  if (a_bytes + r_bytes + b_bytes > 0) {
     std::lock_guard<std::mutex> lk(g_mu);
     const int rc = grow(&ds->lora_mm, &ds->lora_mm_bytes, a_bytes + r_bytes + b_bytes);
     if (rc != LTX25_OK) { return rc; }
+    base = (char*)ds->lora_mm;
   }
-  char* base = (char*)ds->lora_mm;
   const uint16_t* pa = (const uint16_t*)a;
-  uint16_t* pr = (uint16_t*)(base + a_bytes);
+  uint16_t* pr = own_r ? (uint16_t*)(base + a_bytes) : (uint16_t*)r_caller;
   const uint16_t* pb = (const uint16_t*)b;
   if (pad_a) {
     // A [rank][K] -> [rk][K]: one row of rank*K elements, zero-filled to rk*K
@@ -551,6 +558,7 @@ int lora_pair(DeviceState* ds, hipStream_t st, const void* x, const void* a, con
     if (half == 0) {
       d.x = (const uint16_t*)x;
       d.w = pa;
+      d.wn = pad_a ? rk : rank;
       d.y = pr;
       d.N = rk;
       d.K = K;
@@ -562,7 +570,10 @@ int lora_pair(DeviceState* ds, hipStream_t st, const void* x, const void* a, con
       d.N = N;
       d.K = rk;
     }
-    const ltx25::GemmPlan plan = ltx25::plan_gemm(d.M, d.N, d.K, d.bits, ds->cu_count);
+    const ltx25::GemmPlan plan =
+        half == 0 ? r_plan
+                  : ltx25::plan_gemm(d.M, d.N, d.K, d.bits, ds->cu_count,
+                                     g_tile.load(std::memory_order_relaxed));
     float* ws = nullptr;
     if (plan.workspace_bytes > 0) {
       std::lock_guard<std::mutex> lk(g_mu);
@@ -657,13 +668,11 @@ int run_fold(DeviceState* ds, hipStream_t st, const FoldPlan& f, const void* x,
     wd = (uint16_t*)ds->deq;
     base = (char*)ds->lora_mm;
   }
-  // [W | B]: the expansion at row stride K + rk, B in each row's last rk columns
-  hipError_t e = ltx25::launch_dequant(w->codes, (const uint16_t*)w->scales,
-                                       (const uint16_t*)w->qbias, w->bits, w->group, wd, N, K,
-                                       st, kt, (const uint16_t*)b, rank, rank);
-  if (e != hipSuccess) { return hip_fail(e, "fold: dequant launch"); }
-  // r = bf16(x . A^T) over A padded to rk rows
+  // r = bf16(x . A^T), then [W | B]: both ahead of the main GEMM on `st` (on
+  // a second stream beside the expansion they were measured slower: the two
+  // kernels slow each other and the fork / join costs ~19 us of gaps)
   const uint16_t* pa = (const uint16_t*)a;
+  hipError_t e = hipSuccess;
   if (pad_a) {
     e = ltx25::launch_lora_pad(pa, 1, rank * K, rank * K, (uint16_t*)base, rk * K, st);
     if (e != hipSuccess) { return hip_fail(e, "fold: A pad launch"); }
@@ -682,6 +691,10 @@ int run_fold(DeviceState* ds, hipStream_t st, const FoldPlan& f, const void* x,
   rd.K = K;
   e = ltx25::launch_gemm(rd, f.r_plan, ws, st);
   if (e != hipSuccess) { return hip_fail(e, "fold: r gemm launch"); }
+  // [W | B]: the expansion at row stride K + rk, B in each row's last rk columns
+  e = ltx25::launch_dequant(w->codes, (const uint16_t*)w->scales, (const uint16_t*)w->qbias,
+                            w->bits, w->group, wd, N, K, st, kt, (const uint16_t*)b, rank, rank);
+  if (e != hipSuccess) { return hip_fail(e, "fold: dequant launch"); }
   // y = epi([x | r] . [W | B]^T + bias)
   ltx25::GemmDesc d;
   d.x = (const uint16_t*)x;
@@ -923,7 +936,6 @@ int ltx25_lora_route(const void* x, const void* a, const void* b, const void* y,
 int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
                    void* y, void* r, void* d, int M, int K, int N, int rank)
 {
-  (void)r;
   (void)d;
   // The reference returns without encoding anything for an empty shape
   // (src/ltx25-metal-ops.cc:996).
@@ -940,7 +952,7 @@ int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
   const int rc = current_device(&ds);
   if (rc != LTX25_OK) { return rc; }
   if (route == LTX25_LORA_PAIR) {
-    return lora_pair(ds, (hipStream_t)stream, x, a, b, y, M, K, N, rank);
+    return lora_pair(ds, (hipStream_t)stream, x, a, b, y, r, M, K, N, rank);
   }
   const int rank8 = (rank + 7) & ~7;
   const bool vec = lora_vec_ok(M, K, N, rank, x, a, y);
@@ -964,8 +976,10 @@ int ltx25_lora_add(void* stream, const void* x, const void* a, const void* b,
     // [rank][K] weight of that linear), then the fused kernel's second
     // phase reads it -- instead of recomputing x . A^T for every column
     // split of a row block. Same roundings (r rounded once to bf16).
-    uint16_t* rb = nullptr;
-    {
+    // r goes to the caller's buffer when it has one ([M][rank], 16-byte
+    // aligned), else to the library's scratch
+    uint16_t* rb = (uint16_t*)r;
+    if (rb == nullptr || !aligned16(rb)) {
       std::lock_guard<std::mutex> lk(g_mu);
       const int rc2 = grow(&ds->lora_mm, &ds->lora_mm_bytes, (size_t)M * rank * 2);
       if (rc2 != LTX25_OK) { return rc2; }

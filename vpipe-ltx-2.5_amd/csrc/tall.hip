@@ -88,6 +88,7 @@ struct TallParams {
   const uint16_t* qbias;   // w8 mode: bf16 [N][K / group]
   int gshift, gcols;       // w8 mode: log2(group), K / group
   uint16_t* y;
+  const uint16_t* y_in;    // bf16 mode without x2, optional: the accumulators start from it
   int M, N, K;             // K in elements
   int wn;                  // rows of w in memory; rows past them read as zeros
   int bias_type, epilogue;
@@ -237,6 +238,34 @@ tall_kernel(TallParams p)
       for (int r = 0; r < 4; ++r) { acc[i][j][r] = 0; }
     }
   }
+  // Accumulate into an existing output (the LoRA pair's second GEMM,
+  // y = bf16(y + r . B^T)): the accumulators start from y_in in their own
+  // layout (block (i, j), lane l: row 16 i + l % 16 of the group's half,
+  // four consecutive columns from 16 j + 4 (l / 16) of the wave's), so the
+  // K loop adds the products to it and the epilogue rounds once, as the
+  // template tile does. The loads are issued before any operand load, so
+  // the hand-counted vmcnt waits below only ever wait longer for them.
+  if constexpr (!I8 && !FOLD) {
+    if (p.y_in != nullptr) {
+      const int lrow = lane & 15;
+      const int lcol = (lane >> 4) * 4;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int m = m0 + g * 128 + i * 16 + lrow;
+        if (m >= p.M) { continue; }
+        const uint16_t* const yrow = p.y_in + (size_t)m * p.N;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int nn = n0 + wn * 64 + j * 16 + lcol;
+          if (nn >= p.N) { continue; }   // N % 8 == 0: all four columns or none
+          const uint2 o = *(const uint2*)(yrow + nn);
+          acc[i][j] = f32x4v{__uint_as_float(o.x << 16), __uint_as_float(o.x & 0xffff0000u),
+                             __uint_as_float(o.y << 16), __uint_as_float(o.y & 0xffff0000u)};
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   auto compute = [&]() {
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -712,12 +741,14 @@ hipError_t launch_tall(const TallParams& p, int mode, hipStream_t stream)
 
 bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan)
 {
-  // The template keeps the accumulating output and rows that are not whole
-  // 16-byte chunks. The per-lane byte offsets are 32-bit, rows past the last
+  // The template keeps rows that are not whole 16-byte chunks and an
+  // accumulating output beside the two-part activation or off 8-byte
+  // alignment. The per-lane byte offsets are 32-bit, rows past the last
   // tile's end included.
   return plan.tile == 0 && plan.splits == 1 && d.bits == 16 &&
          (d.x2 == nullptr || (d.kx > 0 && d.kx < d.K && d.kx % kBK == 0)) &&
-         d.y_in == nullptr && d.N % 8 == 0 && d.K % kBK == 0 && d.K >= kBK &&
+         (d.y_in == nullptr || (d.x2 == nullptr && ((uintptr_t)d.y_in & 7u) == 0)) &&
+         d.N % 8 == 0 && d.K % kBK == 0 && d.K >= kBK &&
          (size_t)(d.M + kBM) * d.K * 2 < kFourGib && (size_t)(d.N + kBN) * d.K * 2 < kFourGib;
 }
 
@@ -761,7 +792,8 @@ hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream)
   if (d.M < 1 || d.N < 8 || d.N % 8 != 0 || d.K < kBK || d.K % kBK != 0 || d.bits != 16 ||
       (size_t)d.M * d.K * 2 >= kTwoGib || (size_t)d.N * d.K * 2 >= kTwoGib ||
       (size_t)d.M * d.N * 2 >= kTwoGib ||
-      (d.x2 != nullptr && (d.kx <= 0 || d.kx >= d.K || d.kx % kBK != 0))) {
+      (d.x2 != nullptr && (d.kx <= 0 || d.kx >= d.K || d.kx % kBK != 0)) ||
+      (d.y_in != nullptr && (d.x2 != nullptr || ((uintptr_t)d.y_in & 7u) != 0))) {
     return hipErrorInvalidValue;
   }
   TallParams p = {};
@@ -771,6 +803,7 @@ hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream)
   p.w = d.w;
   p.bias = d.bias;
   p.y = d.y;
+  p.y_in = d.y_in;
   p.M = d.M;
   p.N = d.N;
   p.K = d.K;
