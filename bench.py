@@ -1016,6 +1016,52 @@ def kernel_grid_summary(trace_csv, out, cmd, note):
     print("\n".join(lines))
 
 
+def ceilings_summary(json_path, trace_csv, out, cmd):
+    """bench.py --ceilings-only output (the rates) and its rocprofv3 kernel trace (the probe
+    kernels' own durations) -> one markdown summary."""
+    import csv
+    import statistics
+
+    with open(json_path) as f:
+        c = json.loads([ln for ln in f.read().splitlines() if ln.startswith("{")][-1])["ceilings"]
+    groups = {}
+    with open(trace_csv) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+            if "probe" not in name and "stream" not in name:
+                continue
+            key = (name, int(r.get("Grid_Size", r.get("Grid_Size_X", 0))))
+            groups.setdefault(key, []).append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = ["# The library's own ceilings: streaming read and MFMA stream", "",
+             "Commands (MI355X box, repo root):", "", "```", cmd,
+             f"python3 bench.py --ceilings-summary <json> <out>/run_kernel_trace.csv {out} '<cmd>'",
+             "```", "",
+             "Streaming read (`ltx25_probe_read`: 16-byte non-temporal loads, one word per "
+             "workgroup to a sink, rotated over a 384 MB pool so no launch reads what the last "
+             "one did; the fastest of grids 256-2048, best of interleaved rounds):", "",
+             "| bytes of | bytes | grid (workgroups) | best us | best GB/s | median GB/s |",
+             "|---|---|---|---|---|---|"]
+    for name, v in c["read"].items():
+        lines.append(f"| {name} | {v['bytes']} | {v['grid']} | {v['best_us']:.2f} | "
+                     f"{v['best_GBps']:.0f} | {v['median_GBps']:.0f} |")
+    lines += ["", "MFMA stream (`ltx25_probe_mfma`: v_mfma_f32_16x16x32_bf16 back to back on 8 "
+              "accumulators, 256 workgroups, zero or xorshift-random bf16 operands):", "",
+              "| operands, waves per SIMD | best ms | TFLOP/s | fraction of the 2.5 PFLOP/s peak |",
+              "|---|---|---|---|"]
+    for name, v in c["mfma_stream"].items():
+        lines.append(f"| {name} | {v['best_ms']:.3f} | {v['TFLOPs']:.0f} | "
+                     f"{v['frac_bf16_peak']:.3f} |")
+    lines += ["", "Probe kernels in the trace:", "",
+              "| kernel | grid (threads) | calls | median us | min us |", "|---|---|---|---|---|"]
+    for (name, grid), v in sorted(groups.items()):
+        lines.append(f"| `{name}` | {grid} | {len(v)} | {statistics.median(v):.2f} | "
+                     f"{min(v):.2f} |")
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1052,7 +1098,13 @@ def main():
     ap.add_argument("--busy-summary", nargs=3, metavar=("CSV", "OUT_MD", "CMD"),
                     help="summarise a rocprofv3 --pmc run of GRBM_GUI_ACTIVE, "
                          "SQ_VALU_MFMA_BUSY_CYCLES and TCC_BUSY_avr into OUT_MD and exit")
+    ap.add_argument("--ceilings-summary", nargs=4, metavar=("JSON", "TRACE_CSV", "OUT_MD", "CMD"),
+                    help="summarise a --ceilings-only run and its rocprofv3 kernel trace into "
+                         "OUT_MD and exit")
     args = ap.parse_args()
+    if args.ceilings_summary:
+        ceilings_summary(*args.ceilings_summary)
+        return
     if args.busy_summary:
         busy_summary(*args.busy_summary)
         return

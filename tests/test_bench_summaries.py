@@ -64,3 +64,33 @@ def test_kernel_grid_summary_writes_the_roofline_figures(bench, tmp_path, monkey
     flop = 2.0 * 8160 * 4096 * 16384
     assert got["tflops"] == pytest.approx(flop / 806e-6 / 1e12, abs=0.01)
     assert got["frac"] == pytest.approx(got["tflops"] / 2500.0, abs=1e-4)
+
+
+def test_ceilings_summary_carries_rates_and_probe_kernels(bench, tmp_path):
+    c = {"ceilings": {
+        "read": {"qkv": {"bytes": 1600, "grid": 512, "best_us": 5.0, "best_GBps": 3200.0,
+                         "median_GBps": 3000.0, "by_grid_best_us": {"512": 5.0}}},
+        "mfma_stream": {"random_2wave": {"best_ms": 1.0, "TFLOPs": 2100.0,
+                                         "frac_bf16_peak": 0.84}}}}
+    js = tmp_path / "ceil.json"
+    js.write_text("[bench] a log line\n" + json.dumps(c) + "\n")
+    rows = [{"Kernel_Name": "ltx25::(anonymous namespace)::stream_read_kernel(int)",
+             "Grid_Size_X": 131072, "Start_Timestamp": 0, "End_Timestamp": 5000},
+            {"Kernel_Name": "void ltx25::(anonymous namespace)::mfma_stream_kernel<true>(int)",
+             "Grid_Size_X": 131072, "Start_Timestamp": 0, "End_Timestamp": 1000000},
+            {"Kernel_Name": "ltx25::dequant_kernel<8>(int)", "Grid_Size_X": 64,
+             "Start_Timestamp": 0, "End_Timestamp": 1000}]
+    trace = tmp_path / "run_kernel_trace.csv"
+    with open(trace, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    out = tmp_path / "ceilings.md"
+    bench.ceilings_summary(str(js), str(trace), str(out), "the command")
+    text = out.read_text()
+    assert "| qkv | 1600 | 512 | 5.00 | 3200 | 3000 |" in text
+    assert "| random_2wave | 1.000 | 2100 | 0.840 |" in text
+    assert "`ltx25::stream_read_kernel` | 131072 | 1 | 5.00" in text
+    assert "mfma_stream_kernel<true>" in text
+    assert "dequant_kernel" not in text
+    assert "the command" in text
