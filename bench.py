@@ -314,9 +314,9 @@ def bench_audio(pkg, torch, steps, warmup, sets=6):
     pass_ms = float(np.median([a.elapsed_time(b) for a, b in passes]))
     stream_ms = pass_ms / sets
     # The read ceiling for each GEMM's byte count: the library's own streaming-read probe
-    # (ltx25_probe_read: 16-byte loads, four in flight per lane, each workgroup on its own
-    # span), the best over grids of 256..2048 workgroups, its source rotated through a
-    # 384 MB pool so that the 256 MB memory-side cache cannot serve repeats.
+    # (ltx25_probe_read: 16-byte loads, four in flight per lane, one workgroup per 16 KB),
+    # back to back in a captured burst, its source rotated through a 384 MB pool so that
+    # the 256 MB memory-side cache cannot serve repeats.
     reads = read_ceiling(pkg, torch, [(name, gbytes(M, K, N)) for name, K, N in AUDIO], steps)
     return {
         "GBps": gbs,
@@ -332,9 +332,12 @@ def bench_audio(pkg, torch, steps, warmup, sets=6):
     }
 
 
-def read_ceiling(pkg, torch, sizes, steps):
-    """ltx25_probe_read at each (name, bytes): best and median time over interleaved rounds,
-    per grid size, and the grid that reads fastest."""
+def read_ceiling(pkg, torch, sizes, steps, burst=24):
+    """ltx25_probe_read at each (name, bytes), one workgroup per 16 KB (so each byte count
+    has a launch shape of its own in a kernel trace), its source rotated through a 384 MB
+    pool so that the 256 MB memory-side cache cannot serve repeats. Timed as a captured
+    burst of `burst` back-to-back launches over distinct slots (per launch: the replay's
+    time / burst; the host's launch cost is out of it), best and median over replays."""
     pool = torch.ones((384 << 20,), dtype=torch.uint8, device="cuda")
     sink = torch.empty((65536,), dtype=torch.int32, device="cuda")
     out = {}
@@ -342,21 +345,31 @@ def read_ceiling(pkg, torch, sizes, steps):
         nbytes = (nbytes + 15) // 16 * 16
         span = (nbytes + 4095) // 4096 * 4096
         slots = (pool.numel() - span) // span
-        arms = {}
-        for blocks in (256, 512, 1024, 2048):
-            i = [0]
-
-            def rd(blocks=blocks, i=i):
-                off = (i[0] % slots) * span
-                pkg.probe_read(pool[off:], nbytes, sink, blocks)
-                i[0] += 1
-            arms[blocks] = rd
-        r = interleaved(torch, arms, rounds=max(20, steps * 2))
-        best = min(r, key=lambda b: r[b]["best_ms"])
-        out[name] = {"bytes": nbytes, "grid": best, "best_us": r[best]["best_ms"] * 1e3,
-                     "best_GBps": nbytes / (r[best]["best_ms"] * 1e-3) / 1e9,
-                     "median_GBps": nbytes / (r[best]["median_ms"] * 1e-3) / 1e9,
-                     "by_grid_best_us": {b: v["best_ms"] * 1e3 for b, v in r.items()}}
+        blocks = min(65535, (nbytes + 16383) // 16384)
+        views = [pool[(i % slots) * span:] for i in range(burst)]
+        for v in views[:4]:
+            pkg.probe_read(v, nbytes, sink, blocks)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for v in views:
+                pkg.probe_read(v, nbytes, sink, blocks)
+        graph.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(max(10, steps)):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            graph.replay()
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b) / burst)
+        del graph
+        best, med = min(times), float(np.median(times))
+        out[name] = {"bytes": nbytes, "grid": blocks, "best_us": best * 1e3,
+                     "best_GBps": nbytes / (best * 1e-3) / 1e9,
+                     "median_GBps": nbytes / (med * 1e-3) / 1e9}
     del pool
     return out
 
@@ -1037,9 +1050,10 @@ def ceilings_summary(json_path, trace_csv, out, cmd):
              "Commands (MI355X box, repo root):", "", "```", cmd,
              f"python3 bench.py --ceilings-summary <json> <out>/run_kernel_trace.csv {out} '<cmd>'",
              "```", "",
-             "Streaming read (`ltx25_probe_read`: 16-byte non-temporal loads, one word per "
-             "workgroup to a sink, rotated over a 384 MB pool so no launch reads what the last "
-             "one did; the fastest of grids 256-2048, best of interleaved rounds):", "",
+             "Streaming read (`ltx25_probe_read`: 16-byte non-temporal loads, one workgroup per "
+             "16 KB, one word per workgroup to a sink, rotated over a 384 MB pool so no launch "
+             "reads what the last one did; per launch = a captured burst of 24 back-to-back "
+             "launches / 24, best and median of the replays):", "",
              "| bytes of | bytes | grid (workgroups) | best us | best GB/s | median GB/s |",
              "|---|---|---|---|---|---|"]
     for name, v in c["read"].items():

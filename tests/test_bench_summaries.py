@@ -69,7 +69,7 @@ def test_kernel_grid_summary_writes_the_roofline_figures(bench, tmp_path, monkey
 def test_ceilings_summary_carries_rates_and_probe_kernels(bench, tmp_path):
     c = {"ceilings": {
         "read": {"qkv": {"bytes": 1600, "grid": 512, "best_us": 5.0, "best_GBps": 3200.0,
-                         "median_GBps": 3000.0, "by_grid_best_us": {"512": 5.0}}},
+                         "median_GBps": 3000.0}},
         "mfma_stream": {"random_2wave": {"best_ms": 1.0, "TFLOPs": 2100.0,
                                          "frac_bf16_peak": 0.84}}}}
     js = tmp_path / "ceil.json"
