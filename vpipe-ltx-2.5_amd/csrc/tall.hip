@@ -33,11 +33,11 @@
 //   - X rows 0..127 are read only by group 0 and rows 128..255 only by
 //     group 1, so X has two stages per half and the weight, read by both
 //     groups, three (32 + 32 + 96 KB = the 160 KB of LDS). Group 0 loads
-//     the X half group 1 reads and a quarter... (each wave 4 of the 32
-//     weight load instructions), group 1 the other X half and the other
-//     weight share, each at the start of its memory cluster, so every load
-//     has three or more phases (about 1.5 us) to land. The exact vmcnt each
-//     wave waits for is derived per phase below.
+//     the X half group 1 reads and group 1 the X half group 0 reads; each
+//     wave also loads 4 of the 32 weight load instructions of a step. Each
+//     group issues its loads at the start of its memory cluster, so every
+//     load has three or more phases (about 1.5 us) to land. The exact vmcnt
+//     each wave waits for is derived per phase below.
 //   - Per step and CU the fragment reads move 192 KB through LDS and the
 //     loads 64 KB into it (measured costs ~4.6 ns per 1 KB read, ~1.9 ns per
 //     1 KB load interleaved with reads): ~1 us of LDS time against ~1.1 us
