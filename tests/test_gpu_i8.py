@@ -51,6 +51,39 @@ def test_quantize_rows_bit_exact(pkg, M, K):
     assert np.array_equal(q.cpu().numpy(), q_ref)
 
 
+def test_quantize_rows_at_half_integer_quotients(pkg):
+    """Values whose quotient v / s sits on or next to a half-integer: the
+    quantizer's reciprocal fast path must hand these to the division (ties
+    to even, and the nearest integer on either side of a tie)."""
+    K = 512
+    rows = []
+    r0 = np.zeros(K, np.float32)   # amax 127: s = 1 exactly, exact ties
+    ties = np.array([2.5, -3.5, 0.5, -0.5, 1.5, 126.5, -126.5, 64.5, -65.5, 100.5], np.float32)
+    r0[:ties.size] = ties
+    r0[ties.size] = 127.0
+    rows.append(r0)
+    for amax in (1.0, 0.75, 3.0, 1e-3, 5e4):   # s = amax / 127: quotients next to the ties
+        s = np.float32(amax) / np.float32(127.0)
+        k = (np.arange(K) % 254) - 127
+        r = ((k + 0.5) * s).astype(np.float32)
+        r[0] = amax
+        rows.append(r)
+    # (amax, v) where v * fl(1 / s) rounds to the other side of 63.5 than v / s
+    # does (found by an exhaustive search over bf16 values)
+    for amax, v in ((27.0, 13.5), (1.6640625, 0.83203125), (91.5, 45.75), (72.0, 36.0),
+                    (87.5, 43.75), (15.0625, 7.53125)):
+        r = np.zeros(K, np.float32)
+        r[0], r[1], r[2] = amax, v, -v
+        rows.append(r)
+    x = orc.bf16_rne(np.stack(rows))
+    M = x.shape[0]
+    say(f"i8 quantize rows at half-integer quotients M={M} K={K}")
+    q, sc = quantize_rows_dev(pkg, dev_bf16(x), M, K)
+    q_ref, s_ref = orc.i8_quantize_rows(x)
+    assert np.array_equal(sc.cpu().numpy(), s_ref)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
 @pytest.mark.parametrize("N,K,bits,group", [
     (48, 2048, 8, 64), (40, 4096, 8, 32), (33, 4096, 4, 64), (17, 2048, 4, 32),
     (6, 36864, 8, 64),     # w8: 2304 chunks per row, past the register cache

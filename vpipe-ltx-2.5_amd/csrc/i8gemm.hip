@@ -15,39 +15,50 @@ namespace ltx25 {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kRowsPerBlock = kThreads / 64;   // one wave per row
 
-// Rows longer than kCacheChunks 16-byte chunks per thread are re-read for
-// the second pass; up to that they stay in registers between the passes.
-constexpr int kCacheChunks = 8;
+// 16-byte chunks a lane keeps in registers between the absmax pass and the
+// quantize pass (K up to 8192 bf16 or 16384 w8 codes); chunks past them are
+// read again for the second pass.
+constexpr int kCacheChunks = 16;
 
-__device__ __forceinline__ uint32_t q8(float v, float s)
+// q = clamp(rint(v / s), -127, 127) with v / s correctly rounded, given
+// rs = 1 / s rounded. t = v * rs is within 2^-24 |v / s| (1 + 2^-24) of the
+// quotient, i.e. within 2^-15 for |t| < 256; so rint(t) = rint(v / s)
+// unless t lies within 2^-13 of a half-integer. Those values, and any t that
+// is not a finite number below 256 (s tiny, v or s not finite), take the
+// division itself.
+__device__ __forceinline__ uint32_t q8(float v, float s, float rs)
 {
   float r = 0.0f;
   if (s > 0.0f) {
-    r = rintf(v / s);
+    const float t = v * rs;
+    r = rintf(t);
+    if (!(fabsf(t) < 256.0f) || fabsf(t - r) > 0.5f - 0x1p-13f) { r = rintf(v / s); }
     r = fminf(fmaxf(r, -127.0f), 127.0f);
   }
   return (uint32_t)(int)r & 0xffu;
 }
 
-__device__ __forceinline__ float block_absmax(float amax, float* red)
+__device__ __forceinline__ float wave_absmax(float amax)
 {
   for (int off = 32; off > 0; off >>= 1) {
     amax = fmaxf(amax, __shfl_xor(amax, off, 64));
   }
-  if ((threadIdx.x & 63) == 0) { red[threadIdx.x >> 6] = amax; }
-  __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  return amax;
 }
 
-// One workgroup per row: absmax, then q = clamp(rint(x / s), -127, 127),
-// s = absmax / 127. Works on bf16 activations (values exact in f32); the
-// row is read once, 16 bytes (8 values) per load.
+// One wave per row: absmax, then q = clamp(rint(x / s), -127, 127),
+// s = absmax / 127. Works on bf16 activations (values exact in f32). Lane l
+// takes 16-byte chunks l, l + 64, ...: every load instruction of the wave
+// covers 1 KB of the row, up to 16 of them in flight per lane, and the
+// row's maximum is a shuffle reduction (no LDS, no barrier).
 __global__ void __launch_bounds__(kThreads)
-i8_quantize_rows_kernel(const uint16_t* x, int8_t* q, float* scale, int K)
+i8_quantize_rows_kernel(const uint16_t* x, int8_t* q, float* scale, int M, int K)
 {
-  __shared__ float red[kThreads / 64];
-  const int m = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (m >= M) { return; }
   const uint16_t* xr = x + (size_t)m * K;
   int8_t* qr = q + (size_t)m * K;
   const int chunks = K / 8;
@@ -63,51 +74,54 @@ i8_quantize_rows_kernel(const uint16_t* x, int8_t* q, float* scale, int K)
   };
 #pragma unroll
   for (int c = 0; c < kCacheChunks; ++c) {
-    const int i = (int)threadIdx.x + c * kThreads;
-    if (i < chunks) {
-      cache[c] = *(const uint4*)(xr + (size_t)i * 8);
-      absmax8(cache[c]);
-    }
+    const int i = lane + c * 64;
+    if (i < chunks) { cache[c] = *(const uint4*)(xr + (size_t)i * 8); }
   }
-  for (int i = (int)threadIdx.x + kCacheChunks * kThreads; i < chunks; i += kThreads) {
+#pragma unroll
+  for (int c = 0; c < kCacheChunks; ++c) {
+    if (lane + c * 64 < chunks) { absmax8(cache[c]); }
+  }
+  for (int i = lane + kCacheChunks * 64; i < chunks; i += 64) {
     absmax8(*(const uint4*)(xr + (size_t)i * 8));
   }
-  amax = block_absmax(amax, red);
+  amax = wave_absmax(amax);
   const float s = amax / 127.0f;
-  if (threadIdx.x == 0) { scale[m] = s; }
+  const float rs = 1.0f / s;
+  if (lane == 0) { scale[m] = s; }
   auto quant8 = [&](const uint4& v, int i) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     uint32_t packed[2] = {0u, 0u};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint16_t h = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
-      packed[j >> 2] |= q8(bf16_to_f32(h), s) << (8 * (j & 3));
+      packed[j >> 2] |= q8(bf16_to_f32(h), s, rs) << (8 * (j & 3));
     }
     *(uint2*)(qr + (size_t)i * 8) = make_uint2(packed[0], packed[1]);
   };
 #pragma unroll
   for (int c = 0; c < kCacheChunks; ++c) {
-    const int i = (int)threadIdx.x + c * kThreads;
+    const int i = lane + c * 64;
     if (i < chunks) { quant8(cache[c], i); }
   }
-  for (int i = (int)threadIdx.x + kCacheChunks * kThreads; i < chunks; i += kThreads) {
+  for (int i = lane + kCacheChunks * 64; i < chunks; i += 64) {
     quant8(*(const uint4*)(xr + (size_t)i * 8), i);
   }
 }
 
 // The same for the dequantized values of a group-affine weight row,
-// w = bf16(fma(scale, q, qbias)): one 16-byte load of codes (16 w8 or 32 w4
-// codes, all in one group) per chunk, kept in registers between the absmax
-// and the quantize pass; 16-byte int8 stores.
+// w = bf16(fma(scale, q, qbias)): one wave per row, one 16-byte load of
+// codes (16 w8 or 32 w4 codes, all in one group) per chunk, kept in
+// registers between the absmax and the quantize pass; 16-byte int8 stores.
 template <int BITS>
 __global__ void __launch_bounds__(kThreads)
 i8_quantize_qweight_kernel(const uint8_t* codes, const uint16_t* scales,
                            const uint16_t* qbias, int gshift, int gcols,
-                           int8_t* q, float* scale, int K)
+                           int8_t* q, float* scale, int N, int K)
 {
-  __shared__ float red[kThreads / 64];
   constexpr int CPC = 128 / BITS;                 // codes per 16-byte chunk
-  const int n = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (n >= N) { return; }
   const uint8_t* cr = codes + (size_t)n * ((size_t)K * BITS / 8);
   const uint16_t* srow = scales + (size_t)n * gcols;
   const uint16_t* brow = qbias + (size_t)n * gcols;
@@ -140,26 +154,29 @@ i8_quantize_qweight_kernel(const uint8_t* codes, const uint16_t* scales,
   };
 #pragma unroll
   for (int c = 0; c < kCacheChunks; ++c) {
-    const int i = (int)threadIdx.x + c * kThreads;
-    if (i < chunks) {
-      cache[c] = *(const uint4*)(cr + (size_t)i * 16);
-      absmax_chunk(cache[c], i);
-    }
+    const int i = lane + c * 64;
+    if (i < chunks) { cache[c] = *(const uint4*)(cr + (size_t)i * 16); }
   }
-  for (int i = (int)threadIdx.x + kCacheChunks * kThreads; i < chunks; i += kThreads) {
+#pragma unroll
+  for (int c = 0; c < kCacheChunks; ++c) {
+    const int i = lane + c * 64;
+    if (i < chunks) { absmax_chunk(cache[c], i); }
+  }
+  for (int i = lane + kCacheChunks * 64; i < chunks; i += 64) {
     absmax_chunk(*(const uint4*)(cr + (size_t)i * 16), i);
   }
-  amax = block_absmax(amax, red);
+  amax = wave_absmax(amax);
   const float s = amax / 127.0f;
-  if (threadIdx.x == 0) { scale[n] = s; }
+  const float rs = 1.0f / s;
+  if (lane == 0) { scale[n] = s; }
   auto quant_chunk = [&](const uint4& c, int i) {
     float v[CPC];
     dequant(c, i, v);
     uint32_t packed[CPC / 4];
 #pragma unroll
     for (int t = 0; t < CPC / 4; ++t) {
-      packed[t] = q8(v[4 * t], s) | (q8(v[4 * t + 1], s) << 8) | (q8(v[4 * t + 2], s) << 16) |
-                  (q8(v[4 * t + 3], s) << 24);
+      packed[t] = q8(v[4 * t], s, rs) | (q8(v[4 * t + 1], s, rs) << 8) |
+                  (q8(v[4 * t + 2], s, rs) << 16) | (q8(v[4 * t + 3], s, rs) << 24);
     }
 #pragma unroll
     for (int t = 0; t < CPC / 16; ++t) {
@@ -169,10 +186,10 @@ i8_quantize_qweight_kernel(const uint8_t* codes, const uint16_t* scales,
   };
 #pragma unroll
   for (int c = 0; c < kCacheChunks; ++c) {
-    const int i = (int)threadIdx.x + c * kThreads;
+    const int i = lane + c * 64;
     if (i < chunks) { quant_chunk(cache[c], i); }
   }
-  for (int i = (int)threadIdx.x + kCacheChunks * kThreads; i < chunks; i += kThreads) {
+  for (int i = lane + kCacheChunks * 64; i < chunks; i += 64) {
     quant_chunk(*(const uint4*)(cr + (size_t)i * 16), i);
   }
 }
@@ -189,8 +206,8 @@ int ilog2(int v)
 hipError_t launch_i8_quantize_rows(const uint16_t* x, int8_t* q, float* s,
                                    int M, int K, hipStream_t stream)
 {
-  hipLaunchKernelGGL(i8_quantize_rows_kernel, dim3(M), dim3(kThreads), 0,
-                     stream, x, q, s, K);
+  const dim3 grid((unsigned)((M + kRowsPerBlock - 1) / kRowsPerBlock));
+  hipLaunchKernelGGL(i8_quantize_rows_kernel, grid, dim3(kThreads), 0, stream, x, q, s, M, K);
   return hipGetLastError();
 }
 
@@ -202,14 +219,13 @@ hipError_t launch_i8_quantize_qweight(const void* codes,
 {
   const int gshift = ilog2(group);
   const int gcols = K / group;
+  const dim3 grid((unsigned)((N + kRowsPerBlock - 1) / kRowsPerBlock));
   if (bits == 8) {
-    hipLaunchKernelGGL(i8_quantize_qweight_kernel<8>, dim3(N), dim3(kThreads),
-                       0, stream, (const uint8_t*)codes, scales, qbias, gshift,
-                       gcols, q, s, K);
+    hipLaunchKernelGGL(i8_quantize_qweight_kernel<8>, grid, dim3(kThreads), 0, stream,
+                       (const uint8_t*)codes, scales, qbias, gshift, gcols, q, s, N, K);
   } else {
-    hipLaunchKernelGGL(i8_quantize_qweight_kernel<4>, dim3(N), dim3(kThreads),
-                       0, stream, (const uint8_t*)codes, scales, qbias, gshift,
-                       gcols, q, s, K);
+    hipLaunchKernelGGL(i8_quantize_qweight_kernel<4>, grid, dim3(kThreads), 0, stream,
+                       (const uint8_t*)codes, scales, qbias, gshift, gcols, q, s, N, K);
   }
   return hipGetLastError();
 }
