@@ -375,46 +375,88 @@ tall_kernel(TallParams p)
   const int lrow = lane & 15;
   const int lcol = (lane >> 4) * 4;
   uint16_t* const stage = (uint16_t*)lds;
-  float sxm[8];
-  if constexpr (I8) {
+  // The epilogue's operands -- bias, and the int8 mode's row and column
+  // scales -- are loaded together before any is used, at indices clamped
+  // into range (a column or row past the end is never stored): no branch
+  // sits between the loads, so they are waited for once, not one by one.
+  float b4s[4][4], sw4s[4][4], sxm[8];
+  {
+    int ncl[4][4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int m = m0 + g * 128 + i * 16 + lrow;
-      sxm[i] = m < p.M ? p.sx[m] : 0.0f;
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int nn = n0 + wn * 64 + j * 16 + lcol + t;
+        ncl[j][t] = nn < p.N ? nn : p.N - 1;
+      }
+    }
+    if (p.bias_type == kBiasF32) {
+      const float* const bf = (const float*)p.bias;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) { b4s[j][t] = bf[ncl[j][t]]; }
+      }
+    } else if (p.bias_type == kBiasBf16) {
+      const uint16_t* const bh = (const uint16_t*)p.bias;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) { b4s[j][t] = bf16_to_f32(bh[ncl[j][t]]); }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) { b4s[j][t] = 0.0f; }
+      }
+    }
+    if constexpr (I8) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) { sw4s[j][t] = p.sw[ncl[j][t]]; }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int m = m0 + g * 128 + i * 16 + lrow;
+        sxm[i] = p.sx[m < p.M ? m : p.M - 1];
+      }
+      if (p.acc_out != nullptr) {
+        // the raw int32 accumulators, when asked for (bit-exact checks);
+        // N % 8 == 0, so the four columns are all in range
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int m = m0 + g * 128 + i * 16 + lrow;
+            const int nn = n0 + wn * 64 + j * 16 + lcol;
+            if (m < p.M && nn < p.N) {
+              int32_t* arow = p.acc_out + (size_t)m * p.N + nn;
+#pragma unroll
+              for (int t = 0; t < 4; ++t) { arow[t] = acc[i][j][t]; }
+            }
+          }
+        }
+      }
     }
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = wn * 64 + j * 16 + lcol;
-    float b4[4], sw4[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int nn = n0 + c + t;
-      b4[t] = nn < p.N ? load_bias(p.bias, p.bias_type, nn) : 0.0f;
-      if constexpr (I8) { sw4[t] = nn < p.N ? p.sw[nn] : 0.0f; }
-    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = g * 128 + i * 16 + lrow;
       float v[4];
       if constexpr (I8) {
-        const int m = m0 + r;
-        const int nn = n0 + c;
-        if (p.acc_out != nullptr && m < p.M && nn < p.N) {
-          // the raw int32 accumulators, when asked for (bit-exact checks);
-          // N % 8 == 0, so the four columns are all in range
-          int32_t* arow = p.acc_out + (size_t)m * p.N + nn;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) { arow[t] = acc[i][j][t]; }
-        }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           // y = bf16(fma(float(acc), sx[m] * sw[n], bias[n])), that order
-          v[t] = fmaf((float)acc[i][j][t], sxm[i] * sw4[t], b4[t]);
+          v[t] = fmaf((float)acc[i][j][t], sxm[i] * sw4s[j][t], b4s[j][t]);
         }
       } else {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) { v[t] = acc[i][j][t] + b4[t]; }
+        for (int t = 0; t < 4; ++t) { v[t] = acc[i][j][t] + b4s[j][t]; }
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
