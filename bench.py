@@ -36,6 +36,7 @@ import ctypes
 import importlib.util
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -394,6 +395,132 @@ def bench_ceilings(pkg, torch, steps):
                 "best_ms": r["best_ms"], "TFLOPs": flop / (r["best_ms"] * 1e-3) / 1e12,
                 "frac_bf16_peak": flop / (r["best_ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
     return {"read": reads, "mfma_stream": mfma}
+
+
+# The M <= 128 kernel's phase boundaries, in stamp order (ltx25_probe_skinny_phases)
+SKINNY_PHASES = ["codes in registers", "scale block in LDS", "K loop", "partials summed",
+                 "stores complete"]
+SKINNY_PHASE_CASES = [("qkv", 2048, 6144, 0), ("out", 2048, 2048, 0), ("out", 2048, 2048, 1024),
+                      ("out", 2048, 2048, 512), ("ff_up", 2048, 8192, 0),
+                      ("ff_down", 8192, 2048, 0)]
+
+
+def bench_skinny_phases(pkg, torch, steps, sets=6):
+    """The audio GEMMs (and the out GEMM forced to 2 and 4 K splits) through the M <= 128
+    kernel's phase-stamp instantiation: per case, back-to-back calls over `sets` rotated
+    weight sets, the last `sets` calls stamped. Per wave: the time from entry to each phase
+    boundary; per call: the span from the first wave's entry to the last wave's end (100 MHz
+    clock)."""
+    M = 126
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    xs = {K: torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16) for K in (2048, 8192)}
+    out = {}
+    for name, K, N, k_chunk in SKINNY_PHASE_CASES:
+        ws = [(make_qweight(pkg, torch, N, K, g),
+               torch.randn((N,), device="cuda", generator=g) * 0.01,
+               torch.empty((M, N), dtype=torch.bfloat16, device="cuda")) for _ in range(sets)]
+        tiles = (N + 31) // 32
+        nwords = 4 * tiles * 8 * 10            # room for 4 splits
+        stamps = [torch.zeros((nwords,), dtype=torch.int64, device="cuda") for _ in range(sets)]
+        splits = 0
+
+        def call(i):
+            qw, b, y = ws[i % sets]
+            return pkg.probe_skinny_phases(xs[K], qw, b, y, M, K, N, k_chunk,
+                                           stamps[i % sets], nwords * 8)
+
+        for i in range(2 * sets):
+            call(i)
+        torch.cuda.synchronize()
+        for i in range(max(4, steps) * sets):
+            splits = call(i)
+        torch.cuda.synchronize()
+        nwg = splits * tiles
+        st = np.stack([s.cpu().numpy()[: nwg * 80].reshape(nwg, 8, 10) for s in stamps])
+        clk = st[..., :6].astype(np.float64)
+        rt0 = st[..., 6].astype(np.float64)
+        rt1 = st[..., 7].astype(np.float64)
+        ok = rt1 > rt0
+        ghz = float(np.median((clk[..., 5] - clk[..., 0])[ok] / ((rt1 - rt0)[ok] * 10.0)))
+        phases = np.diff(clk, axis=-1) / ghz / 1e3                   # us, [call][wg][wave][5]
+        span = (rt1.max(axis=(1, 2)) - rt0.min(axis=(1, 2))) * 10.0 / 1e3
+        start = (rt0.min(axis=2) - rt0.min(axis=(1, 2))[:, None]) * 10.0 / 1e3   # per WG
+        hw = st[..., 0, 8]
+        cu = (st[..., 0, 9] & 0xF) * 4096 + ((hw >> 13) & 7) * 256 + ((hw >> 12) & 1) * 16 + \
+            ((hw >> 8) & 0xF)
+        per_cu = max(int(np.unique(c, return_counts=True)[1].max()) for c in cu)
+        out[f"{name} k_chunk={k_chunk or 'plan'}"] = {
+            "name": name, "K": K, "N": N, "k_chunk": k_chunk, "splits": splits,
+            "workgroups": nwg,
+            "clock_GHz": ghz, "span_us_median": float(np.median(span)),
+            "wg_start_us_p90": float(np.percentile(start, 90)),
+            "max_workgroups_per_cu": per_cu,
+            "phase_us_median": {p: float(np.median(phases[..., i]))
+                                for i, p in enumerate(SKINNY_PHASES)},
+            "phase_us_p90": {p: float(np.percentile(phases[..., i], 90))
+                             for i, p in enumerate(SKINNY_PHASES)}}
+        del ws, stamps
+    return out
+
+
+def skinny_phases_summary(json_path, trace_csv, out, cmd):
+    """bench.py --skinny-phases-only output (stamps) and its rocprofv3 kernel trace (the
+    stamped kernels' and their reductions' durations, in case order) -> one markdown file."""
+    import csv
+    import statistics
+
+    with open(json_path) as f:
+        c = json.loads([ln for ln in f.read().splitlines() if ln.startswith("{")][-1])
+    c = c["skinny_phases"]
+    # One case = one run of launches of the stamped kernel (and their reductions) with no
+    # other kernel between them: each case's set-up (its weights) launches kernels first.
+    runs = []
+    with open(trace_csv) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    apart = True
+    for r in rows:
+        name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+        dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        if re.search(r"skinny_kernel<\d+, (true|false), true>$", name):
+            key = (int(r.get("Grid_Size_X", r.get("Grid_Size", 0))), int(r.get("Grid_Size_Y", 1)))
+            if apart or runs[-1]["key"] != key:
+                runs.append({"key": key, "main": [], "reduce": []})
+            runs[-1]["main"].append(dur)
+            apart = False
+        elif "splitk_reduce" in name and runs and not apart:
+            runs[-1]["reduce"].append(dur)
+        else:
+            apart = True
+    lines = ["# Phase stamps of the M <= 128 kernel (the audio GEMMs, M = 126, w8g64)", "",
+             "Commands (MI355X box, repo root):", "", "```", cmd,
+             f"python3 bench.py --skinny-phases-summary <json> <out>/run_kernel_trace.csv {out} "
+             "'<cmd>'", "```", "",
+             "`ltx25_probe_skinny_phases` runs the same kernel as the linear's M <= 128 route, "
+             "instantiated with stamps: lane 0 of each wave reads the shader clock at entry and "
+             "at five phase boundaries and the 100 MHz clock at entry and end. Each case runs "
+             "over six rotated weight sets, 60 calls after 12 warm-up calls; the last six are "
+             "stamped. "
+             "Phase times are medians (p90) over all waves of those calls; the span runs from "
+             "the first wave's entry to the last wave's end; rocprof is the dispatch's own "
+             "duration, which adds launch and drain to the span.", "",
+             "| case | splits | workgroups | " + " | ".join(SKINNY_PHASES) +
+             " | span us | rocprof main us | rocprof reduce us |",
+             "|---|---|---|" + "---|" * len(SKINNY_PHASES) + "---|---|---|"]
+    for (key, v), run in zip(c.items(), runs + [None] * len(c)):
+        ph = " | ".join(f"{v['phase_us_median'][p]:.2f} ({v['phase_us_p90'][p]:.2f})"
+                        for p in SKINNY_PHASES)
+        main = f"{statistics.median(run['main']):.2f}" if run else "-"
+        red = f"{statistics.median(run['reduce']):.2f}" if run and run["reduce"] else "-"
+        lines.append(f"| {key} | {v['splits']} | {v['workgroups']} | {ph} | "
+                     f"{v['span_us_median']:.2f} | {main} | {red} |")
+    lines += ["", "Clock under load (shader clock ticks per 100 MHz tick): " +
+              ", ".join(f"{k} {v['clock_GHz']:.2f} GHz" for k, v in c.items()) + ".",
+              "Workgroups per CU at most: " +
+              ", ".join(f"{k} {v['max_workgroups_per_cu']}" for k, v in c.items()) + "."]
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
 
 
 # ---- next rows: the LoRA delta and the dequant-once A/B arm ------------------------------
@@ -1115,9 +1242,19 @@ def main():
     ap.add_argument("--ceilings-summary", nargs=4, metavar=("JSON", "TRACE_CSV", "OUT_MD", "CMD"),
                     help="summarise a --ceilings-only run and its rocprofv3 kernel trace into "
                          "OUT_MD and exit")
+    ap.add_argument("--skinny-phases-only", action="store_true",
+                    help="run only the M <= 128 kernel's phase-stamp probe over the audio GEMMs "
+                         "and print the stamps as one JSON line")
+    ap.add_argument("--skinny-phases-summary", nargs=4,
+                    metavar=("JSON", "TRACE_CSV", "OUT_MD", "CMD"),
+                    help="summarise a --skinny-phases-only run and its rocprofv3 kernel trace "
+                         "into OUT_MD and exit")
     args = ap.parse_args()
     if args.ceilings_summary:
         ceilings_summary(*args.ceilings_summary)
+        return
+    if args.skinny_phases_summary:
+        skinny_phases_summary(*args.skinny_phases_summary)
         return
     if args.busy_summary:
         busy_summary(*args.busy_summary)
@@ -1147,6 +1284,10 @@ def main():
 
     if args.ceilings_only:
         print(json.dumps({"ceilings": bench_ceilings(pkg, torch, args.steps)}), flush=True)
+        return
+    if args.skinny_phases_only:
+        print(json.dumps({"skinny_phases": bench_skinny_phases(pkg, torch, args.steps)}),
+              flush=True)
         return
     log(f"FFN pair (config 2): warmup {args.warmup}, steps {args.steps}")
     ffn = bench_ffn(pkg, torch, args.steps, args.warmup, same_tensors=not args.skip_hipblaslt)

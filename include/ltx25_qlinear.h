@@ -486,6 +486,26 @@ int ltx25_probe_read(void* stream, const void* src, size_t bytes, void* sink, in
  * the practically impossible case that a sum equals 1.2345. iters > 0. */
 int ltx25_probe_mfma(void* stream, int iters, int random, int waves_per_simd, void* out);
 
+/* Per-phase clock stamps of the M <= 128 kernel (the audio GEMMs' route):
+ * one w8 linear y = x . dequant(w)^T (+ bias) with M <= 128, through the
+ * same kernel as ltx25_linear_q's M <= 128 route, instantiated with stamps
+ * (the instantiations linear runs carry none). k_chunk is the K per
+ * workgroup: 0 for the planner's split, else a multiple of 64 up to 2048,
+ * which forces ceil(K / k_chunk) splits (their f32 partials in the
+ * library's workspace, then the split-K reduction launch, as in linear).
+ * Lane 0 of each wave writes ten u64 to `stamps` (device) at
+ * [(split * ceil(N / 32) + tile) * 8 + wave] * 10: the shader clock
+ * (s_memtime) at entry, codes in registers, the workgroup's scale block in
+ * LDS, K loop done, the eight partial tiles summed, stores complete; the
+ * 100 MHz clock (s_memrealtime) at entry and at the end; the HW_ID and
+ * XCC_ID registers. stamps_bytes must hold splits * ceil(N / 32) * 640
+ * bytes; *splits_out (host) receives the splits. Operand rules as for
+ * ltx25_linear_q; LTX25_E_UNSUPPORTED when the shape is not on the
+ * M <= 128 route or the weight is not w8. */
+int ltx25_probe_skinny_phases(void* stream, const void* x, const ltx25_qweight* w,
+                              const void* bias, int bias_dtype, void* y, int M, int K, int N,
+                              int k_chunk, void* stamps, size_t stamps_bytes, int* splits_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -94,3 +94,50 @@ def test_ceilings_summary_carries_rates_and_probe_kernels(bench, tmp_path):
     assert "mfma_stream_kernel<true>" in text
     assert "dequant_kernel" not in text
     assert "the command" in text
+
+
+def test_skinny_phases_summary_matches_cases_to_trace_runs(bench, tmp_path):
+    """Cases map, in order, to consecutive runs of the stamped kernel in the trace (two
+    cases of one grid shape stay apart), each run's reductions to its case; the product
+    kernel's launches are not counted."""
+    ph = {p: 1.0 for p in bench.SKINNY_PHASES}
+    def case(name, splits, wg):
+        return {"name": name, "K": 2048, "N": 2048, "k_chunk": 0, "splits": splits,
+                "workgroups": wg, "clock_GHz": 2.2,
+                "span_us_median": 9.0, "wg_start_us_p90": 0.3, "max_workgroups_per_cu": 1,
+                "phase_us_median": ph, "phase_us_p90": ph}
+    c = {"skinny_phases": {"out k_chunk=plan": case("out", 1, 64),
+                           "out k_chunk=512": case("out", 4, 256),
+                           "ff_down k_chunk=plan": case("ff_down", 4, 256)}}
+    js = tmp_path / "ph.json"
+    js.write_text(json.dumps(c) + "\n")
+    stamped = "void ltx25::(anonymous namespace)::skinny_kernel<8, {}, true>(ltx25::SParams)"
+    rows, t = [], 0
+    def add(name, gx, gy, us):
+        nonlocal t
+        rows.append({"Kernel_Name": name, "Grid_Size_X": gx, "Grid_Size_Y": gy,
+                     "Start_Timestamp": t, "End_Timestamp": t + int(us * 1000)})
+        t += 100000
+    for _ in range(3):
+        add(stamped.format("false"), 32768, 1, 10.0)
+    add("void ltx25::(anonymous namespace)::skinny_kernel<8, false, false>(ltx25::SParams)",
+        32768, 1, 50.0)
+    for _ in range(3):
+        add(stamped.format("true"), 32768, 4, 8.5)
+        add("ltx25::splitk_reduce_kernel(float const*)", 64512, 1, 3.5)
+    add("void at::native::fill_kernel(int)", 256, 1, 1.0)
+    for _ in range(3):
+        add(stamped.format("true"), 32768, 4, 13.5)
+        add("ltx25::splitk_reduce_kernel(float const*)", 64512, 1, 4.0)
+    trace = tmp_path / "run_kernel_trace.csv"
+    with open(trace, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    out = tmp_path / "phases.md"
+    bench.skinny_phases_summary(str(js), str(trace), str(out), "the command")
+    text = out.read_text()
+    assert "| out k_chunk=plan | 1 | 64 |" in text and "| 9.00 | 10.00 | - |" in text
+    assert "| out k_chunk=512 | 4 | 256 |" in text and "| 9.00 | 8.50 | 3.50 |" in text
+    assert "| ff_down k_chunk=plan | 4 | 256 |" in text and "| 9.00 | 13.50 | 4.00 |" in text
+    assert "50.00" not in text and "the command" in text

@@ -36,3 +36,58 @@ def test_probe_mfma_runs(pkg, dev, random, wps):
     say(f"probe_mfma random={random} waves_per_simd={wps}")
     pkg.probe_mfma(100, random, wps, out)
     torch.cuda.synchronize()
+
+
+# (M, K, N, k_chunk, splits): the planner's split, forced 2- and 4-way splits, K > 2048
+PHASE_CASES = [(126, 2048, 96, 0, 1), (126, 2048, 64, 1024, 2), (100, 2048, 40, 512, 4),
+               (126, 8192, 64, 0, 4)]
+
+
+@pytest.mark.parametrize("M,K,N,k_chunk,splits", PHASE_CASES)
+def test_probe_skinny_phases(pkg, dev, M, K, N, k_chunk, splits):
+    """The phase-stamp instantiation computes what the linear computes (bit for bit: the
+    same sums in the same order, plus clock reads) and writes ordered stamps for every wave
+    of every workgroup, the split count included."""
+    from gpu_util import make_qweight, rng_normal
+    rng = np.random.default_rng(M + K + N + k_chunk)
+    qw = make_qweight(pkg, rng_normal(rng, (N, K), 0.02), 8, 64)[0]
+    x = torch.from_numpy(rng_normal(rng, (M, K))).to(torch.bfloat16).cuda()
+    bias = torch.from_numpy(rng_normal(rng, (N,), 0.1)).cuda()
+    tiles = (N + 31) // 32
+    nwords = splits * tiles * 8 * 10
+    stamps = torch.zeros((nwords + 80,), dtype=torch.int64, device="cuda")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    say(f"probe_skinny_phases M={M} K={K} N={N} k_chunk={k_chunk}")
+    got_splits = pkg.probe_skinny_phases(x, qw, bias, y, M, K, N, k_chunk, stamps, nwords * 8)
+    torch.cuda.synchronize()
+    assert got_splits == splits
+    want = torch.empty_like(y)
+    if k_chunk == 0:
+        pkg.linear_q(x, qw, bias, want, M, K, N)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+    else:
+        # a forced split sums the same products in another order: the oracle's tolerance
+        # (bf16 rounding of the f32 sum) against the linear's own result
+        pkg.linear_q(x, qw, bias, want, M, K, N)
+        torch.cuda.synchronize()
+        assert torch.allclose(y.float(), want.float(), rtol=1e-2, atol=1e-2)
+    s = stamps.cpu().numpy()
+    assert not s[nwords:].any(), "stamps written past splits * tiles * 8 waves"
+    s = s[:nwords].reshape(splits * tiles, 8, 10)
+    clk = s[..., :6]
+    assert (np.diff(clk, axis=-1) >= 0).all(), "shader-clock stamps out of phase order"
+    assert (s[..., 7] >= s[..., 6]).all() and (s[..., 6] > 0).all()
+
+
+def test_probe_skinny_phases_rejects(pkg, dev):
+    from gpu_util import make_qweight, rng_normal
+    rng = np.random.default_rng(5)
+    qw = make_qweight(pkg, rng_normal(rng, (64, 2048), 0.02), 8, 64)[0]
+    x = torch.zeros((126, 2048), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((126, 64), dtype=torch.bfloat16, device="cuda")
+    stamps = torch.zeros((4 * 2 * 8 * 10,), dtype=torch.int64, device="cuda")
+    for k_chunk, nbytes in ((100, stamps.numel() * 8), (4096, stamps.numel() * 8),
+                            (512, 2 * 8 * 10 * 8 * 3)):   # 4 splits need 4 x 2 tiles
+        with pytest.raises(pkg.Ltx25Error):
+            pkg.probe_skinny_phases(x, qw, None, y, 126, 2048, 64, k_chunk, stamps, nbytes)

@@ -104,6 +104,8 @@ SIGNATURES = {
     "ltx25_gate_heads": (_i, [_vp, _vp, _vp, _i, _i, _i]),
     "ltx25_probe_read": (_i, [_vp, _vp, _sz, _vp, _i]),
     "ltx25_probe_mfma": (_i, [_vp, _i, _i, _i, _vp]),
+    "ltx25_probe_skinny_phases": (_i, [_vp, _vp, ctypes.POINTER(QWeightC), _vp, _i, _vp, _i, _i,
+                                       _i, _i, _vp, _sz, ctypes.POINTER(ctypes.c_int)]),
     "ltx25_dequant": (_i, [_vp, ctypes.POINTER(QWeightC), _vp, _i, _i]),
     "ltx25_set_dequant_once": (_i, [_i]),
     "ltx25_dequant_once_takes": (_i, [_i, _i, _i]),
@@ -275,6 +277,18 @@ def probe_mfma(iters: int, random: bool, waves_per_simd: int, out, stream=None) 
     """The MFMA-stream ceiling probe (ltx25_probe_mfma)."""
     check(load().ltx25_probe_mfma(_stream(stream), iters, 1 if random else 0, waves_per_simd,
                                   _ptr(out)))
+
+
+def probe_skinny_phases(x, w: QWeight, bias, y, M: int, K: int, N: int, k_chunk: int, stamps,
+                        stamps_bytes: int, stream=None) -> int:
+    """One w8 linear on the M <= 128 kernel's phase-stamp instantiation
+    (ltx25_probe_skinny_phases); returns the number of K splits."""
+    cw = w.c()
+    splits = ctypes.c_int(0)
+    check(load().ltx25_probe_skinny_phases(_stream(stream), _ptr(x), ctypes.byref(cw), _ptr(bias),
+                                           bias_dtype_of(bias), _ptr(y), M, K, N, k_chunk,
+                                           _ptr(stamps), stamps_bytes, ctypes.byref(splits)))
+    return splits.value
 
 
 def dequant(w: QWeight, out, N: int, K: int, stream=None) -> None:

@@ -1106,6 +1106,76 @@ int ltx25_probe_mfma(void* stream, int iters, int random, int waves_per_simd, vo
   return e == hipSuccess ? LTX25_OK : hip_fail(e, "probe mfma launch");
 }
 
+int ltx25_probe_skinny_phases(void* stream, const void* x, const ltx25_qweight* w,
+                              const void* bias, int bias_dtype, void* y, int M, int K, int N,
+                              int k_chunk, void* stamps, size_t stamps_bytes, int* splits_out)
+{
+  if (x == nullptr || y == nullptr || stamps == nullptr || splits_out == nullptr) {
+    return fail(LTX25_E_INVAL, "x, y, stamps or splits_out is null");
+  }
+  int rc = check_shape(M, K, N);
+  if (rc != LTX25_OK) { return rc; }
+  rc = check_qweight(w, K);
+  if (rc != LTX25_OK) { return rc; }
+  if (!w->quantized || w->bits != 8) {
+    return fail(LTX25_E_UNSUPPORTED, "the phase stamps are built for w8 weights only");
+  }
+  if (!bias_ok(bias, bias_dtype)) {
+    return fail(LTX25_E_INVAL, "bias dtype %d is not valid for a %s bias",
+                bias_dtype, bias == nullptr ? "null" : "non-null");
+  }
+  if ((rc = check_aligned("x", x)) != LTX25_OK || (rc = check_aligned("y", y)) != LTX25_OK ||
+      (rc = check_aligned("weight", w->codes)) != LTX25_OK) {
+    return rc;
+  }
+  if (k_chunk < 0 || k_chunk % 64 != 0 || k_chunk > 2048) {
+    return fail(LTX25_E_INVAL, "k_chunk=%d: 0, or a multiple of 64 up to 2048", k_chunk);
+  }
+  DeviceState* ds = nullptr;
+  rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  ltx25::GemmPlan plan;
+  if (K % 64 != 0 || !ltx25::plan_skinny(M, N, K, 8, ds->cu_count, plan)) {
+    return fail(LTX25_E_UNSUPPORTED, "M=%d K=%d N=%d is not on the M <= 128 route", M, K, N);
+  }
+  if (k_chunk > 0) {
+    plan.k_chunk = k_chunk;
+    plan.splits = (K + k_chunk - 1) / k_chunk;
+    plan.workspace_bytes = plan.splits > 1 ? (size_t)plan.splits * M * N * sizeof(float) : 0;
+  }
+  const size_t tiles = (size_t)(N + 31) / 32;
+  const size_t need = (size_t)plan.splits * tiles * 8 * 10 * sizeof(unsigned long long);
+  if (stamps_bytes < need) {
+    return fail(LTX25_E_INVAL, "stamps_bytes=%zu; %d splits x %zu tiles need %zu", stamps_bytes,
+                plan.splits, tiles, need);
+  }
+  float* ws = nullptr;
+  if (plan.workspace_bytes > 0) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    rc = grow(&ds->ws, &ds->ws_bytes, plan.workspace_bytes);
+    if (rc != LTX25_OK) { return rc; }
+    ws = (float*)ds->ws;
+  }
+  ltx25::GemmDesc d;
+  d.x = (const uint16_t*)x;
+  d.w = w->codes;
+  d.scales = (const uint16_t*)w->scales;
+  d.qbias = (const uint16_t*)w->qbias;
+  d.bits = 8;
+  d.group = w->group;
+  d.bias = bias;
+  d.bias_type = bias != nullptr ? bias_dtype : ltx25::kBiasNone;
+  d.epilogue = ltx25::kEpiNone;
+  d.y = (uint16_t*)y;
+  d.M = M;
+  d.N = N;
+  d.K = K;
+  *splits_out = plan.splits;
+  const hipError_t e = ltx25::launch_skinny(d, plan, ws, (hipStream_t)stream,
+                                            (unsigned long long*)stamps);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "skinny phase-stamp launch");
+}
+
 int ltx25_set_i8_gemm(int on)
 {
   g_i8_on.store(on != 0 ? 1 : 0, std::memory_order_relaxed);

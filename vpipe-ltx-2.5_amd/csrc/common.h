@@ -137,8 +137,10 @@ hipError_t launch_gemm(const GemmDesc& d, const GemmPlan& plan,
 // between its 8 waves, and across workgroups above 2048. Fills `plan` and
 // returns true when it takes the shape (up to 3 workgroups per CU).
 bool plan_skinny(int M, int N, int K, int bits, int cu_count, GemmPlan& plan);
+// `stamps` non-null (w8 only): the phase-stamp instantiation, ten words per
+// wave at [(split * ceil(N / 32) + tile) * 8 + wave] * 10 (ltx25_probe_skinny_phases)
 hipError_t launch_skinny(const GemmDesc& d, const GemmPlan& plan, float* workspace,
-                         hipStream_t stream);
+                         hipStream_t stream, unsigned long long* stamps = nullptr);
 // The dense bf16 GEMM of the 256 x 256 tile on v_mfma_f32_16x16x32_bf16
 // (tall.hip): the dequant-once arm and dense weights, also with the LoRA
 // fold's two-part activation [x | r] (kx a multiple of 64); not y_in;

@@ -76,7 +76,19 @@ struct SParams {
   int gshift, gcols;
   int k_chunk;              // K per workgroup (multiple of 64)
   int bias_type, epilogue;
+  // the phase-stamp build only (STAMPS): 10 words per wave, see below
+  unsigned long long* stamps;
 };
+
+// Phase stamps (the STAMPS instantiation, for ltx25_probe_skinny_phases):
+// the shader clock at a phase boundary, with the scheduler held on both
+// sides so that the read stays where the source puts it.
+#define LTX25_STAMP(var)                 \
+  if constexpr (STAMPS) {                \
+    __builtin_amdgcn_sched_barrier(0);   \
+    var = __builtin_amdgcn_s_memtime();  \
+    __builtin_amdgcn_sched_barrier(0);   \
+  }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, size_t bytes)
 {
@@ -118,7 +130,7 @@ __device__ __forceinline__ bf16x8 dequant8(uint32_t lo, uint32_t hi, float s, fl
   return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-template <int BITS, bool SPLIT>
+template <int BITS, bool SPLIT, bool STAMPS = false>
 __global__ void __launch_bounds__(kThreads)
 skinny_kernel(SParams p)
 {
@@ -129,6 +141,17 @@ skinny_kernel(SParams p)
   __shared__ float lds_bias[kCols];
   // the workgroup's scales and zero points [32 rows][groups of its K range]
   __shared__ uint16_t lds_sq[2][kCols * kMaxGroups];
+
+  // phase stamps: shader clock at entry, codes in registers, scale block in
+  // LDS, K loop done, partials summed, stores done; 100 MHz clock at entry
+  // and at the end
+  unsigned long long st[6] = {0, 0, 0, 0, 0, 0};
+  unsigned long long rt0 = 0;
+  if constexpr (STAMPS) {
+    __builtin_amdgcn_sched_barrier(0);
+    rt0 = __builtin_amdgcn_s_memrealtime();
+  }
+  LTX25_STAMP(st[0])
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -271,6 +294,7 @@ skinny_kernel(SParams p)
     }
     // the region is unit 1's: its reads have returned before unit 1 lands
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    LTX25_STAMP(st[1])
   } else {
     // The empty asm statements are the weight's first use, and so the point
     // where the compiler waits for it.
@@ -296,6 +320,7 @@ skinny_kernel(SParams p)
     }
   }
   __syncthreads();   // the scale block is in LDS
+  LTX25_STAMP(st[2])
 
   // fragment reads: unit row 32 j + l32 (block mb = 2 hf + j), 16-byte
   // segment 4 h + s, stored at (4 h + s) ^ ((l32 / 2) % 8)
@@ -357,6 +382,7 @@ skinny_kernel(SParams p)
   }
   // every wave is done reading its X slots before the slots hold partial tiles
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  LTX25_STAMP(st[3])
 
   // ---- the 8 partial tiles, summed through LDS in wave order. Block mb,
   // registers 4g..4g+3 of lane l: row 32 mb + l % 32, columns
@@ -370,6 +396,7 @@ skinny_kernel(SParams p)
     }
   }
   __syncthreads();
+  LTX25_STAMP(st[4])
 
   // thread -> row m (0..127), 8 columns 8 nq .. 8 nq + 7
   const int m = tid >> 2;
@@ -387,52 +414,72 @@ skinny_kernel(SParams p)
       for (int j = 0; j < 4; ++j) { v[4 * hh + j] += a[j]; }
     }
   }
-  if (m >= p.M) { return; }
-  const int n = n0 + 8 * nq;
-  if constexpr (SPLIT) {
-    float* prow = p.partial + ((size_t)split * p.M + m) * p.N;
-    if ((p.N & 3) == 0 && n + 8 <= p.N) {
-      *(f32x4*)(prow + n) = f32x4{v[0], v[1], v[2], v[3]};
-      *(f32x4*)(prow + n + 4) = f32x4{v[4], v[5], v[6], v[7]};
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (n + j < p.N) { prow[n + j] = v[j]; }
-      }
-    }
-  } else {
-    const uint16_t* yin = p.y_in != nullptr ? p.y_in + (size_t)m * p.N : nullptr;
-    uint16_t* yrow = p.y + (size_t)m * p.N;
-    const bool vec = (p.N & 7) == 0 && n + 8 <= p.N;
-    if (yin != nullptr) {
-      if (vec) {
-        const uint4 o = *(const uint4*)(yin + n);
-        const uint32_t e[4] = {o.x, o.y, o.z, o.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[2 * j] += __uint_as_float(e[j] << 16);
-          v[2 * j + 1] += __uint_as_float(e[j] & 0xffff0000u);
-        }
+  if (m < p.M) {
+    const int n = n0 + 8 * nq;
+    if constexpr (SPLIT) {
+      float* prow = p.partial + ((size_t)split * p.M + m) * p.N;
+      if ((p.N & 3) == 0 && n + 8 <= p.N) {
+        *(f32x4*)(prow + n) = f32x4{v[0], v[1], v[2], v[3]};
+        *(f32x4*)(prow + n + 4) = f32x4{v[4], v[5], v[6], v[7]};
       } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          if (n + j < p.N) { v[j] += bf16_to_f32(yin[n + j]); }
+          if (n + j < p.N) { prow[n + j] = v[j]; }
+        }
+      }
+    } else {
+      const uint16_t* yin = p.y_in != nullptr ? p.y_in + (size_t)m * p.N : nullptr;
+      uint16_t* yrow = p.y + (size_t)m * p.N;
+      const bool vec = (p.N & 7) == 0 && n + 8 <= p.N;
+      if (yin != nullptr) {
+        if (vec) {
+          const uint4 o = *(const uint4*)(yin + n);
+          const uint32_t e[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            v[2 * j] += __uint_as_float(e[j] << 16);
+            v[2 * j + 1] += __uint_as_float(e[j] & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            if (n + j < p.N) { v[j] += bf16_to_f32(yin[n + j]); }
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[j] += lds_bias[8 * nq + j];
+        if (p.epilogue == kEpiGelu) { v[j] = gelu_tanh(v[j]); }
+      }
+      if (vec) {
+        *(uint4*)(yrow + n) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                         pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (n + j < p.N) { yrow[n + j] = f32_to_bf16(v[j]); }
         }
       }
     }
+  }
+  if constexpr (STAMPS) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the stores have completed
+    LTX25_STAMP(st[5])
+    const unsigned long long rt1 = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_sched_barrier(0);
+    if (p.stamps != nullptr && lane == 0) {
+      // HW_ID (CU, SH, SE of this wave) and XCC_ID, read from the hardware registers
+      const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+      const unsigned xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);
+      unsigned long long* o =
+          p.stamps + ((size_t)(blockIdx.y * gridDim.x + blockIdx.x) * kWaves + wave) * 10;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      v[j] += lds_bias[8 * nq + j];
-      if (p.epilogue == kEpiGelu) { v[j] = gelu_tanh(v[j]); }
-    }
-    if (vec) {
-      *(uint4*)(yrow + n) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                       pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (n + j < p.N) { yrow[n + j] = f32_to_bf16(v[j]); }
-      }
+      for (int i = 0; i < 6; ++i) { o[i] = st[i]; }
+      o[6] = rt0;
+      o[7] = rt1;
+      o[8] = hw;
+      o[9] = xcc;
     }
   }
 }
@@ -465,10 +512,10 @@ bool plan_skinny(int M, int N, int K, int bits, int cu_count, GemmPlan& plan)
 }
 
 hipError_t launch_skinny(const GemmDesc& d, const GemmPlan& plan, float* workspace,
-                         hipStream_t stream)
+                         hipStream_t stream, unsigned long long* stamps)
 {
   if (plan.tile != 2 || d.M < 1 || d.M > kRows || (d.bits != 8 && d.bits != 4 && d.bits != 16) ||
-      d.K % kChunk != 0 ||
+      (stamps != nullptr && d.bits != 8) || d.K % kChunk != 0 ||
       plan.k_chunk % kChunk != 0 || plan.k_chunk > kWaves * kMaxChunks * kChunk ||
       (long)plan.splits * plan.k_chunk < d.K || (plan.splits > 1 && workspace == nullptr)) {
     return hipErrorInvalidValue;
@@ -492,9 +539,17 @@ hipError_t launch_skinny(const GemmDesc& d, const GemmPlan& plan, float* workspa
   p.gshift = d.bits == 16 ? 0 : gs;
   p.gcols = d.bits == 16 ? 0 : d.K / d.group;
   p.k_chunk = plan.k_chunk;
+  p.stamps = stamps;
   const dim3 grid((unsigned)((d.N + kCols - 1) / kCols), (unsigned)plan.splits, 1);
   const bool split = plan.splits > 1;
-  if (d.bits == 8) {
+  if (stamps != nullptr) {
+    // the phase-stamp instantiation (w8 only), for the probe entry point
+    if (split) {
+      hipLaunchKernelGGL((skinny_kernel<8, true, true>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((skinny_kernel<8, false, true>), grid, dim3(kThreads), 0, stream, p);
+    }
+  } else if (d.bits == 8) {
     if (split) {
       hipLaunchKernelGGL((skinny_kernel<8, true>), grid, dim3(kThreads), 0, stream, p);
     } else {
