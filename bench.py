@@ -464,6 +464,162 @@ def bench_skinny_phases(pkg, torch, steps, sets=6):
     return out
 
 
+TALL_PHASES = ["step 0 landed", "K loop", "output staged", "stores complete"]
+
+
+def _tall_stamp_stats(st, steps):
+    """Stamps [calls][tiles][8 waves][8 words] of the 256 x 256 tile -> per-call spans,
+    per-wave phases (us, at each wave's own clock), per-XCD clock and last end, and the gap
+    between consecutive tiles on one CU (the next tile's first entry after the last wave of
+    the previous one ended)."""
+    clk = st[..., :5].astype(np.float64)
+    rt0 = st[..., 5].astype(np.float64)
+    rt1 = st[..., 6].astype(np.float64)
+    ok = rt1 > rt0
+    ghz_w = np.where(ok, (clk[..., 4] - clk[..., 0]) / np.maximum((rt1 - rt0) * 10.0, 1.0), np.nan)
+    phases = np.diff(clk, axis=-1) / ghz_w[..., None] / 1e3
+    xcc = (st[:, :, 0, 7] >> 32) & 0xF
+    hw = st[:, :, 0, 7] & 0xFFFFFFFF
+    cu = xcc * 4096 + ((hw >> 13) & 7) * 256 + ((hw >> 12) & 1) * 16 + ((hw >> 8) & 0xF)
+    base = rt0.min(axis=(1, 2))[:, None]
+    start = (rt0.min(axis=2) - base) * 0.01        # us, per call and tile
+    end = (rt1.max(axis=2) - base) * 0.01
+    gaps = []
+    for c in range(st.shape[0]):
+        for u in np.unique(cu[c]):
+            idx = np.where(cu[c] == u)[0]
+            idx = idx[np.argsort(start[c, idx])]
+            gaps += [start[c, b] - end[c, a] for a, b in zip(idx[:-1], idx[1:])]
+    per_xcc = {}
+    for x in range(8):
+        m = xcc == x
+        if m.any():
+            per_xcc[str(x)] = {"tiles_per_call": int(m.sum()) // st.shape[0],
+                               "clock_GHz": float(np.nanmedian(ghz_w[m])),
+                               "last_end_us": float(np.median([end[c][m[c]].max()
+                                                               for c in range(st.shape[0])]))}
+    tiles = st.shape[1]
+    return {"tiles": tiles, "waves_per_tile": 8, "k_steps": steps,
+            "span_us_median": float(np.median(end.max(axis=1))),
+            "tile_us_p50_p90": [float(np.percentile(end - start, q)) for q in (50, 90)],
+            "tiles_per_cu": sorted({int(v) for v in np.unique(cu[0], return_counts=True)[1]}),
+            "gap_us_p50_p90": [float(np.percentile(gaps, q)) for q in (50, 90)] if gaps else None,
+            "k_loop_cycles_per_step": float(np.median(clk[..., 2] - clk[..., 1]) / steps),
+            "phase_us_median": {p: float(np.nanmedian(phases[..., i]))
+                                for i, p in enumerate(TALL_PHASES)},
+            "phase_us_p90": {p: float(np.nanpercentile(phases[..., i], 90))
+                             for i, p in enumerate(TALL_PHASES)},
+            "per_xcc": per_xcc}
+
+
+def bench_tall_phases(pkg, torch, steps, calls=3):
+    """The 256 x 256 tile's phase-stamp instantiation on the config-2 FFN GEMMs (dense bf16
+    weights, as the dequant-once route's expansion writes them; up with GELU) and on the
+    config-3 int8 GEMM at N = 4096 / 16384: per case, max(20, steps) warm-up calls (the
+    clock ramps over the first ~30 ms of MFMA load), then `calls` stamped calls."""
+    M, D, H = 8160, 4096, 16384
+    g = torch.Generator(device="cuda")
+    g.manual_seed(6)
+    out = {}
+    x = torch.randn((M, D), device="cuda", generator=g).to(torch.bfloat16)
+    for name, K, N, epi in (("ffn_up (GELU)", D, H, pkg.EPI_GELU_TANH),
+                            ("ffn_down", H, D, pkg.EPI_NONE)):
+        xin = x if K == D else torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+        w = (torch.randn((N, K), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        nb = ((M + 255) // 256) * ((N + 255) // 256) * 512
+        stamps = [torch.zeros((nb // 8,), dtype=torch.int64, device="cuda") for _ in range(calls)]
+        for _ in range(max(20, steps)):
+            pkg.probe_tall_phases(xin, w, None, y, M, K, N, epi, stamps[0], nb)
+        for s in stamps:
+            pkg.probe_tall_phases(xin, w, None, y, M, K, N, epi, s, nb)
+        torch.cuda.synchronize()
+        st = np.stack([s.cpu().numpy().reshape(-1, 8, 8) for s in stamps]).astype(np.int64)
+        out[name] = _tall_stamp_stats(st, K // 64)
+        del xin, w, y, stamps
+    xq = torch.empty((M, D), dtype=torch.int8, device="cuda")
+    sx = torch.empty((M,), dtype=torch.float32, device="cuda")
+    pkg.i8_quantize_rows(x, xq, sx, M, D)
+    for N in (4096, 16384):
+        w = (torch.randn((N, D), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        wq = torch.empty((N, D), dtype=torch.int8, device="cuda")
+        sw = torch.empty((N,), dtype=torch.float32, device="cuda")
+        pkg.i8_quantize_rows(w, wq, sw, N, D)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        nb = ((M + 255) // 256) * ((N + 255) // 256) * 512
+        stamps = [torch.zeros((nb // 8,), dtype=torch.int64, device="cuda") for _ in range(calls)]
+        for _ in range(max(20, steps)):
+            pkg.probe_tall_i8_phases(xq, sx, wq, sw, None, y, M, D, N, stamps[0], nb)
+        for s in stamps:
+            pkg.probe_tall_i8_phases(xq, sx, wq, sw, None, y, M, D, N, s, nb)
+        torch.cuda.synchronize()
+        st = np.stack([s.cpu().numpy().reshape(-1, 8, 8) for s in stamps]).astype(np.int64)
+        out[f"int8 N={N}"] = _tall_stamp_stats(st, D // 128)
+        del w, wq, sw, y, stamps
+    return out
+
+
+def tall_phases_summary(json_path, trace_csv, out, cmd):
+    """bench.py --tall-phases-only output (stamps) and its rocprofv3 kernel trace (the
+    stamped tile's dispatch durations, in case order) -> one markdown file."""
+    import csv
+
+    with open(json_path) as f:
+        c = json.loads([ln for ln in f.read().splitlines() if ln.startswith("{")][-1])
+    c = c["tall_phases"]
+    # one case = one run of launches of the stamped tile with no other kernel between them
+    runs = []
+    with open(trace_csv) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    apart = True
+    for r in rows:
+        name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+        dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        if re.search(r"tall_kernel<\d+, false, true>$", name):
+            if apart:
+                runs.append([])
+            runs[-1].append(dur)
+            apart = False
+        else:
+            apart = True
+    lines = ["# Phase stamps of the 256 x 256 tile (config 2 FFN GEMMs, config 3 int8 GEMM)", "",
+             "Commands (MI355X box, repo root):", "", "```", cmd,
+             f"python3 bench.py --tall-phases-summary <json> <out>/run_kernel_trace.csv {out} "
+             "'<cmd>'", "```", "",
+             "`ltx25_probe_tall_phases` / `ltx25_probe_tall_i8_phases` run the same tile as the "
+             "routes (M = 8160; the FFN weights dense bf16, as the dequant-once expansion "
+             "writes them), instantiated with stamps: lane 0 of each wave reads the shader "
+             "clock at entry, when step 0 has landed, after the K loop, after the output tile "
+             "is staged in LDS and after its stores complete, and the 100 MHz clock at entry "
+             "and end. Three stamped calls per case after the warm-up; phases are medians "
+             "(p90) over all waves, each at its own wave's clock. The stamp build waits for its "
+             "stores before the last stamp; the product tile does not.", "",
+             "| case | tiles | tiles per CU | " + " | ".join(TALL_PHASES) +
+             " | tile us p50 / p90 | K-loop cycles per step | span us | rocprof us |",
+             "|---|---|---|" + "---|" * len(TALL_PHASES) + "---|---|---|---|"]
+    for (key, v), run in zip(c.items(), runs + [None] * len(c)):
+        ph = " | ".join(f"{v['phase_us_median'][p]:.2f} ({v['phase_us_p90'][p]:.2f})"
+                        for p in TALL_PHASES)
+        roc = f"{statistics.median(run[-3:]):.1f}" if run else "-"
+        lines.append(f"| {key} | {v['tiles']} | {'/'.join(map(str, v['tiles_per_cu']))} | {ph} | "
+                     f"{v['tile_us_p50_p90'][0]:.1f} / {v['tile_us_p50_p90'][1]:.1f} | "
+                     f"{v['k_loop_cycles_per_step']:.0f} | {v['span_us_median']:.1f} | {roc} |")
+    lines += ["", "Per XCD (clock under load = shader clock ticks per 100 MHz tick; last end = "
+              "the XCD's last wave, from the call's first entry):", "",
+              "| case | " + " | ".join(f"XCD {x} GHz / last end us" for x in range(8)) + " |",
+              "|---|" + "---|" * 8]
+    for key, v in c.items():
+        cells = [f"{v['per_xcc'][str(x)]['clock_GHz']:.2f} / {v['per_xcc'][str(x)]['last_end_us']:.0f}"
+                 if str(x) in v["per_xcc"] else "-" for x in range(8)]
+        lines.append(f"| {key} | " + " | ".join(cells) + " |")
+    lines += ["", "Gap between consecutive tiles on one CU (us, p50 / p90): " +
+              ", ".join(f"{k} {v['gap_us_p50_p90'][0]:.2f} / {v['gap_us_p50_p90'][1]:.2f}"
+                        for k, v in c.items() if v["gap_us_p50_p90"]) + "."]
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def skinny_phases_summary(json_path, trace_csv, out, cmd):
     """bench.py --skinny-phases-only output (stamps) and its rocprofv3 kernel trace (the
     stamped kernels' and their reductions' durations, in case order) -> one markdown file."""
@@ -1242,6 +1398,13 @@ def main():
     ap.add_argument("--ceilings-summary", nargs=4, metavar=("JSON", "TRACE_CSV", "OUT_MD", "CMD"),
                     help="summarise a --ceilings-only run and its rocprofv3 kernel trace into "
                          "OUT_MD and exit")
+    ap.add_argument("--tall-phases-only", action="store_true",
+                    help="run only the 256 x 256 tile's phase-stamp probes (FFN GEMMs, int8 "
+                         "GEMM) and print the stamps' statistics as one JSON line")
+    ap.add_argument("--tall-phases-summary", nargs=4,
+                    metavar=("JSON", "TRACE_CSV", "OUT_MD", "CMD"),
+                    help="summarise a --tall-phases-only run and its rocprofv3 kernel trace "
+                         "into OUT_MD and exit")
     ap.add_argument("--skinny-phases-only", action="store_true",
                     help="run only the M <= 128 kernel's phase-stamp probe over the audio GEMMs "
                          "and print the stamps as one JSON line")
@@ -1255,6 +1418,9 @@ def main():
         return
     if args.skinny_phases_summary:
         skinny_phases_summary(*args.skinny_phases_summary)
+        return
+    if args.tall_phases_summary:
+        tall_phases_summary(*args.tall_phases_summary)
         return
     if args.busy_summary:
         busy_summary(*args.busy_summary)
@@ -1284,6 +1450,9 @@ def main():
 
     if args.ceilings_only:
         print(json.dumps({"ceilings": bench_ceilings(pkg, torch, args.steps)}), flush=True)
+        return
+    if args.tall_phases_only:
+        print(json.dumps({"tall_phases": bench_tall_phases(pkg, torch, args.steps)}), flush=True)
         return
     if args.skinny_phases_only:
         print(json.dumps({"skinny_phases": bench_skinny_phases(pkg, torch, args.steps)}),

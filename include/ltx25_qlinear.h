@@ -506,6 +506,25 @@ int ltx25_probe_skinny_phases(void* stream, const void* x, const ltx25_qweight* 
                               const void* bias, int bias_dtype, void* y, int M, int K, int N,
                               int k_chunk, void* stamps, size_t stamps_bytes, int* splits_out);
 
+/* Per-phase clock stamps of the 256 x 256 tile (the FFN GEMMs' and the int8
+ * tier's kernel), instantiated with stamps (the instantiations linear and
+ * i8_gemm run carry none). ltx25_probe_tall_phases runs the dense bf16
+ * GEMM y = epi(x . w^T + bias), w bf16 [N][K] (what the dequant-once
+ * route's expansion writes), K % 64 == 0, N % 8 == 0;
+ * ltx25_probe_tall_i8_phases the int8 GEMM of ltx25_i8_gemm (operand rules
+ * as there), K % 128 == 0. Lane 0 of each wave writes eight u64 to `stamps`
+ * (device) at (tile * 8 + wave) * 8, tile = the workgroup id: the shader
+ * clock (s_memtime) at entry, step 0 landed, K loop done, the output tile
+ * staged in LDS, stores complete; the 100 MHz clock (s_memrealtime) at
+ * entry and at the end; (XCC_ID << 32) | HW_ID. stamps_bytes must hold
+ * ceil(M / 256) * ceil(N / 256) * 512 bytes. */
+int ltx25_probe_tall_phases(void* stream, const void* x, const void* w_bf16, const void* bias,
+                            int bias_dtype, void* y, int M, int K, int N, int epilogue,
+                            void* stamps, size_t stamps_bytes);
+int ltx25_probe_tall_i8_phases(void* stream, const int8_t* xq, const float* sx, const int8_t* wq,
+                               const float* sw, const void* bias, int bias_dtype, void* y,
+                               int M, int K, int N, void* stamps, size_t stamps_bytes);
+
 #ifdef __cplusplus
 }
 #endif

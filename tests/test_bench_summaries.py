@@ -141,3 +141,42 @@ def test_skinny_phases_summary_matches_cases_to_trace_runs(bench, tmp_path):
     assert "| out k_chunk=512 | 4 | 256 |" in text and "| 9.00 | 8.50 | 3.50 |" in text
     assert "| ff_down k_chunk=plan | 4 | 256 |" in text and "| 9.00 | 13.50 | 4.00 |" in text
     assert "50.00" not in text and "the command" in text
+
+
+def test_tall_phases_summary_rows_and_runs(bench, tmp_path):
+    """Each case takes the rocprof durations of its own run of the stamped tile; the product
+    tile's launches and other kernels split the runs and are not counted."""
+    ph = {p: 2.0 for p in bench.TALL_PHASES}
+    def case(tiles, clk):
+        return {"tiles": tiles, "waves_per_tile": 8, "k_steps": 64, "span_us_median": 880.0,
+                "tile_us_p50_p90": [100.0, 110.0], "tiles_per_cu": [8],
+                "gap_us_p50_p90": [0.4, 0.7], "k_loop_cycles_per_step": 2318.0,
+                "phase_us_median": ph, "phase_us_p90": ph,
+                "per_xcc": {str(x): {"tiles_per_call": tiles // 8, "clock_GHz": clk,
+                                     "last_end_us": 800.0 + x} for x in range(8)}}
+    c = {"tall_phases": {"ffn_up (GELU)": case(2048, 1.7), "int8 N=4096": case(512, 1.4)}}
+    js = tmp_path / "tp.json"
+    js.write_text(json.dumps(c) + "\n")
+    rows, t = [], 0
+    def add(name, us):
+        nonlocal t
+        rows.append({"Kernel_Name": name, "Grid_Size_X": 1048576, "Grid_Size_Y": 1,
+                     "Start_Timestamp": t, "End_Timestamp": t + int(us * 1000)})
+        t += 2000000
+    for _ in range(4):
+        add("void ltx25::(anonymous namespace)::tall_kernel<0, false, true>(ltx25::TallParams)", 900.0)
+    add("void ltx25::(anonymous namespace)::tall_kernel<0, false, false>(ltx25::TallParams)", 5.0)
+    for _ in range(4):
+        add("void ltx25::(anonymous namespace)::tall_kernel<1, false, true>(ltx25::TallParams)", 140.0)
+    trace = tmp_path / "run_kernel_trace.csv"
+    with open(trace, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    out = tmp_path / "tall.md"
+    bench.tall_phases_summary(str(js), str(trace), str(out), "the command")
+    text = out.read_text()
+    assert "| ffn_up (GELU) | 2048 | 8 |" in text and "| 2318 | 880.0 | 900.0 |" in text
+    assert "| int8 N=4096 | 512 | 8 |" in text and "| 2318 | 880.0 | 140.0 |" in text
+    assert "| ffn_up (GELU) | 1.70 / 800 | 1.70 / 801 |" in text
+    assert "5.0" not in text.split("Per XCD")[0].split("|---|")[-1] and "the command" in text

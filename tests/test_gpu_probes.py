@@ -91,3 +91,86 @@ def test_probe_skinny_phases_rejects(pkg, dev):
                             (512, 2 * 8 * 10 * 8 * 3)):   # 4 splits need 4 x 2 tiles
         with pytest.raises(pkg.Ltx25Error):
             pkg.probe_skinny_phases(x, qw, None, y, 126, 2048, 64, k_chunk, stamps, nbytes)
+
+
+def _check_tall_stamps(st, tiles):
+    s = st.cpu().numpy()
+    assert not s[tiles * 64:].any(), "stamps written past tiles * 8 waves"
+    s = s[:tiles * 64].reshape(tiles, 8, 8)
+    assert (s[..., 5] > 0).all(), "a wave wrote no stamps"
+    assert (np.diff(s[..., :5], axis=-1) >= 0).all(), "shader-clock stamps out of phase order"
+    assert (s[..., 6] >= s[..., 5]).all()
+    assert ((s[..., 7] >> 32) < 8).all()
+
+
+# (M, K, N, bias dtype): whole tiles, and ragged M and N. K <= 512 keeps the dense linear
+# on one K split (the planner splits from 1024 of K), so both sum in the same order.
+TALL_PHASE_CASES = [(512, 256, 512, "f32"), (300, 512, 264, "bf16"), (1024, 512, 2048, None)]
+
+
+@pytest.mark.parametrize("M,K,N,bias_dt", TALL_PHASE_CASES)
+def test_probe_tall_phases(pkg, dev, M, K, N, bias_dt):
+    """The bf16 tile's phase-stamp instantiation gives the bits the dense linear gives (the
+    same sums in the same K order on either tile) and stamps every wave of every tile."""
+    rng = np.random.default_rng(M + K + N)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(torch.bfloat16).cuda()
+    w = torch.from_numpy((rng.standard_normal((N, K)) * 0.05).astype(np.float32)).to(
+        torch.bfloat16).cuda()
+    bias = None
+    if bias_dt is not None:
+        b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float32)).cuda()
+        bias = b.to(torch.bfloat16) if bias_dt == "bf16" else b
+    tiles = ((M + 255) // 256) * ((N + 255) // 256)
+    st = torch.zeros((tiles * 64 + 64,), dtype=torch.int64, device="cuda")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    say(f"probe_tall_phases M={M} K={K} N={N} bias={bias_dt}")
+    pkg.probe_tall_phases(x, w, bias, y, M, K, N, pkg.EPI_NONE, st, tiles * 512)
+    want = torch.empty_like(y)
+    pkg.linear(x, w, bias, want, M, K, N)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+    _check_tall_stamps(st, tiles)
+    st.zero_()
+    pkg.probe_tall_phases(x, w, bias, y, M, K, N, pkg.EPI_GELU_TANH, st, tiles * 512)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
+    _check_tall_stamps(st, tiles)
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 256, 512), (300, 384, 264)])
+def test_probe_tall_i8_phases(pkg, dev, M, K, N):
+    """The int8 tile's phase-stamp instantiation gives the bits ltx25_i8_gemm gives."""
+    rng = np.random.default_rng(M * 7 + N)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(torch.bfloat16).cuda()
+    w = torch.from_numpy((rng.standard_normal((N, K)) * 0.05).astype(np.float32)).to(
+        torch.bfloat16).cuda()
+    xq = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    wq = torch.empty((N, K), dtype=torch.int8, device="cuda")
+    sx = torch.empty((M,), dtype=torch.float32, device="cuda")
+    sw = torch.empty((N,), dtype=torch.float32, device="cuda")
+    pkg.i8_quantize_rows(x, xq, sx, M, K)
+    pkg.i8_quantize_rows(w, wq, sw, N, K)
+    bias = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float32)).cuda()
+    tiles = ((M + 255) // 256) * ((N + 255) // 256)
+    st = torch.zeros((tiles * 64 + 64,), dtype=torch.int64, device="cuda")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    want = torch.empty_like(y)
+    say(f"probe_tall_i8_phases M={M} K={K} N={N}")
+    pkg.probe_tall_i8_phases(xq, sx, wq, sw, bias, y, M, K, N, st, tiles * 512)
+    pkg.i8_gemm(xq, sx, wq, sw, bias, want, None, M, K, N)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+    _check_tall_stamps(st, tiles)
+
+
+def test_probe_tall_phases_rejects(pkg, dev):
+    x = torch.zeros((256, 256), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((256, 256), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((256, 256), dtype=torch.bfloat16, device="cuda")
+    st = torch.zeros((64,), dtype=torch.int64, device="cuda")
+    with pytest.raises(pkg.Ltx25Error):     # one tile needs 512 bytes of stamps
+        pkg.probe_tall_phases(x, w, None, y, 256, 256, 256, pkg.EPI_NONE, st, 511)
+    with pytest.raises(pkg.Ltx25Error):     # K not a multiple of 64
+        pkg.probe_tall_phases(x, w, None, y, 256, 200, 256, pkg.EPI_NONE, st, 512)
+    with pytest.raises(pkg.Ltx25Error):     # unknown epilogue
+        pkg.probe_tall_phases(x, w, None, y, 256, 256, 256, 7, st, 512)

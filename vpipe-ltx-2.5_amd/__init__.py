@@ -106,6 +106,9 @@ SIGNATURES = {
     "ltx25_probe_mfma": (_i, [_vp, _i, _i, _i, _vp]),
     "ltx25_probe_skinny_phases": (_i, [_vp, _vp, ctypes.POINTER(QWeightC), _vp, _i, _vp, _i, _i,
                                        _i, _i, _vp, _sz, ctypes.POINTER(ctypes.c_int)]),
+    "ltx25_probe_tall_phases": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _sz]),
+    "ltx25_probe_tall_i8_phases": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _vp,
+                                        _sz]),
     "ltx25_dequant": (_i, [_vp, ctypes.POINTER(QWeightC), _vp, _i, _i]),
     "ltx25_set_dequant_once": (_i, [_i]),
     "ltx25_dequant_once_takes": (_i, [_i, _i, _i]),
@@ -289,6 +292,24 @@ def probe_skinny_phases(x, w: QWeight, bias, y, M: int, K: int, N: int, k_chunk:
                                            bias_dtype_of(bias), _ptr(y), M, K, N, k_chunk,
                                            _ptr(stamps), stamps_bytes, ctypes.byref(splits)))
     return splits.value
+
+
+def probe_tall_phases(x, w_bf16, bias, y, M: int, K: int, N: int, epilogue: int, stamps,
+                      stamps_bytes: int, stream=None) -> None:
+    """The dense bf16 GEMM on the 256 x 256 tile's phase-stamp instantiation
+    (ltx25_probe_tall_phases)."""
+    check(load().ltx25_probe_tall_phases(_stream(stream), _ptr(x), _ptr(w_bf16), _ptr(bias),
+                                         bias_dtype_of(bias), _ptr(y), M, K, N, epilogue,
+                                         _ptr(stamps), stamps_bytes))
+
+
+def probe_tall_i8_phases(xq, sx, wq, sw, bias, y, M: int, K: int, N: int, stamps,
+                         stamps_bytes: int, stream=None) -> None:
+    """The int8 GEMM on the 256 x 256 tile's phase-stamp instantiation
+    (ltx25_probe_tall_i8_phases)."""
+    check(load().ltx25_probe_tall_i8_phases(_stream(stream), _ptr(xq), _ptr(sx), _ptr(wq),
+                                            _ptr(sw), _ptr(bias), bias_dtype_of(bias), _ptr(y),
+                                            M, K, N, _ptr(stamps), stamps_bytes))
 
 
 def dequant(w: QWeight, out, N: int, K: int, stream=None) -> None:

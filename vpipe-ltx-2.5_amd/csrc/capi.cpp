@@ -1176,6 +1176,92 @@ int ltx25_probe_skinny_phases(void* stream, const void* x, const ltx25_qweight* 
   return e == hipSuccess ? LTX25_OK : hip_fail(e, "skinny phase-stamp launch");
 }
 
+// bytes of the 256 x 256 tile's phase stamps: eight u64 per wave, 8 waves per tile
+static size_t tall_stamp_bytes(int M, int N)
+{
+  return (size_t)((M + 255) / 256) * ((N + 255) / 256) * 8 * 8 * sizeof(unsigned long long);
+}
+
+int ltx25_probe_tall_phases(void* stream, const void* x, const void* w_bf16, const void* bias,
+                            int bias_dtype, void* y, int M, int K, int N, int epilogue,
+                            void* stamps, size_t stamps_bytes)
+{
+  if (x == nullptr || w_bf16 == nullptr || y == nullptr || stamps == nullptr) {
+    return fail(LTX25_E_INVAL, "x, w, y or stamps is null");
+  }
+  int rc = check_shape(M, K, N);
+  if (rc != LTX25_OK) { return rc; }
+  if (!bias_ok(bias, bias_dtype)) {
+    return fail(LTX25_E_INVAL, "bias dtype %d is not valid for a %s bias",
+                bias_dtype, bias == nullptr ? "null" : "non-null");
+  }
+  if (epilogue != LTX25_EPI_NONE && epilogue != LTX25_EPI_GELU_TANH) {
+    return fail(LTX25_E_INVAL, "unknown epilogue %d", epilogue);
+  }
+  if ((rc = check_aligned("x", x)) != LTX25_OK || (rc = check_aligned("y", y)) != LTX25_OK ||
+      (rc = check_aligned("w", w_bf16)) != LTX25_OK) {
+    return rc;
+  }
+  if (K % 64 != 0 || N % 8 != 0) {
+    return fail(LTX25_E_UNSUPPORTED, "K=%d N=%d: the 256 x 256 tile takes K %% 64 == 0 and "
+                "N %% 8 == 0", K, N);
+  }
+  if (stamps_bytes < tall_stamp_bytes(M, N)) {
+    return fail(LTX25_E_INVAL, "stamps_bytes=%zu; M=%d N=%d need %zu", stamps_bytes, M, N,
+                tall_stamp_bytes(M, N));
+  }
+  DeviceState* ds = nullptr;
+  rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  ltx25::GemmDesc d;
+  d.x = (const uint16_t*)x;
+  d.w = w_bf16;
+  d.bits = 16;
+  d.group = 64;
+  d.bias = bias;
+  d.bias_type = bias != nullptr ? bias_dtype : ltx25::kBiasNone;
+  d.epilogue = epilogue;
+  d.y = (uint16_t*)y;
+  d.M = M;
+  d.N = N;
+  d.K = K;
+  const hipError_t e = ltx25::launch_tall_dense(d, (hipStream_t)stream,
+                                                (unsigned long long*)stamps);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "tall phase-stamp launch");
+}
+
+int ltx25_probe_tall_i8_phases(void* stream, const int8_t* xq, const float* sx, const int8_t* wq,
+                               const float* sw, const void* bias, int bias_dtype, void* y,
+                               int M, int K, int N, void* stamps, size_t stamps_bytes)
+{
+  if (xq == nullptr || sx == nullptr || wq == nullptr || sw == nullptr || y == nullptr ||
+      stamps == nullptr) {
+    return fail(LTX25_E_INVAL, "null pointer");
+  }
+  int rc = check_shape(M, K, N);
+  if (rc != LTX25_OK) { return rc; }
+  if (!bias_ok(bias, bias_dtype)) { return fail(LTX25_E_INVAL, "bad bias dtype %d", bias_dtype); }
+  if ((rc = check_aligned("xq", xq)) != LTX25_OK || (rc = check_aligned("wq", wq)) != LTX25_OK) {
+    return rc;
+  }
+  if (!ltx25::tall_i8_takes(M, N, K)) {
+    return fail(LTX25_E_UNSUPPORTED, "M=%d K=%d N=%d: the int8 256 x 256 tile takes K %% 128 "
+                "== 0 and N %% 8 == 0", M, K, N);
+  }
+  if (stamps_bytes < tall_stamp_bytes(M, N)) {
+    return fail(LTX25_E_INVAL, "stamps_bytes=%zu; M=%d N=%d need %zu", stamps_bytes, M, N,
+                tall_stamp_bytes(M, N));
+  }
+  DeviceState* ds = nullptr;
+  rc = current_device(&ds);
+  if (rc != LTX25_OK) { return rc; }
+  const hipError_t e = ltx25::launch_tall_i8(xq, sx, wq, sw, bias,
+                                             bias != nullptr ? bias_dtype : ltx25::kBiasNone,
+                                             ltx25::kEpiNone, (uint16_t*)y, nullptr, M, K, N,
+                                             (hipStream_t)stream, (unsigned long long*)stamps);
+  return e == hipSuccess ? LTX25_OK : hip_fail(e, "tall i8 phase-stamp launch");
+}
+
 int ltx25_set_i8_gemm(int on)
 {
   g_i8_on.store(on != 0 ? 1 : 0, std::memory_order_relaxed);

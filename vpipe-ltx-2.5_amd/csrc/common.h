@@ -143,21 +143,27 @@ hipError_t launch_skinny(const GemmDesc& d, const GemmPlan& plan, float* workspa
                          hipStream_t stream, unsigned long long* stamps = nullptr);
 // The dense bf16 GEMM of the 256 x 256 tile on v_mfma_f32_16x16x32_bf16
 // (tall.hip): the dequant-once arm and dense weights, also with the LoRA
-// fold's two-part activation [x | r] (kx a multiple of 64); not y_in;
-// N % 8 == 0. launch_gemm routes there when it takes.
+// fold's two-part activation [x | r] (kx a multiple of 64), or with y_in
+// (8-byte aligned, without the two-part activation); N % 8 == 0.
+// launch_gemm routes there when it takes.
 bool tall_dense_takes(const GemmDesc& d, const GemmPlan& plan);
 // The same tile with w8 codes (groups of 64 or 32) dequantized in registers
 // once per workgroup before the LDS write: bit-identical to the dense tile
 // over the dequant-once expansion. launch_tall_dense runs either.
 bool tall_w8_takes(const GemmDesc& d, const GemmPlan& plan);
-hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream);
+// `stamps` non-null (bf16 without the two-part activation, or the int8
+// launcher below): the phase-stamp instantiation, eight words per wave at
+// (tile * 8 + wave) * 8 (ltx25_probe_tall_phases)
+hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream,
+                             unsigned long long* stamps = nullptr);
 // The int8 tier's GEMM on the same tile (tall.hip, v_mfma_i32_16x16x64_i8):
 // N % 8 == 0, K a multiple of 128. launch_i8_gemm routes there when the
 // 256 x 256 tiles fill the GPU and it takes the shape.
 bool tall_i8_takes(int M, int N, int K);
 hipError_t launch_tall_i8(const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
                           const void* bias, int bias_type, int epilogue, uint16_t* y,
-                          int32_t* acc, int M, int K, int N, hipStream_t stream);
+                          int32_t* acc, int M, int K, int N, hipStream_t stream,
+                          unsigned long long* stamps = nullptr);
 // The no-allocation linear's split-K scratch (noalloc.hip): a fixed device
 // array of kNoAllocScratchBytes per GPU. noalloc_scratch() returns the
 // current device's copy, resolving its address on the first call there.

@@ -93,6 +93,9 @@ struct TallParams {
   int wn;                  // rows of w in memory; rows past them read as zeros
   int bias_type, epilogue;
   int tiles_m, tiles_n;
+  // the phase-stamp instantiation only (ltx25_probe_tall_phases): eight
+  // words per wave at (tile * 8 + wave) * 8
+  unsigned long long* stamps;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, size_t bytes)
@@ -106,6 +109,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, size_
 #define LTX25_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0f70 | (n))
 // s_waitcnt lgkmcnt(0)
 #define LTX25_LGKMCNT0() __builtin_amdgcn_s_waitcnt(0xc07f)
+// A phase stamp (the STAMPS instantiation): the shader clock, with the
+// scheduler held on both sides so that the read stays where the source puts it
+#define LTX25_TSTAMP(var)                \
+  if constexpr (STAMPS) {                \
+    __builtin_amdgcn_sched_barrier(0);   \
+    var = __builtin_amdgcn_s_memtime();  \
+    __builtin_amdgcn_sched_barrier(0);   \
+  }
 
 // f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>): the
 // index is a compile-time constant inside f
@@ -146,15 +157,25 @@ constexpr int kPPLds = 5 * kOp;
 static_assert(kPPLds == 160 * 1024, "the stages fill the LDS");
 static_assert(kBM * kEP * 2 <= kPPLds, "the staged tile fits the stages");
 
-template <int MODE, bool FOLD>
+template <int MODE, bool FOLD, bool STAMPS = false>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 tall_kernel(TallParams p)
 {
   static_assert(MODE == kModeBf16 || MODE == kModeI8, "w8 codes run tall_w8_kernel");
   static_assert(!FOLD || MODE == kModeBf16, "the two-part activation is a bf16-mode operand");
+  static_assert(!STAMPS || !FOLD, "the phase stamps are built without the two-part activation");
   constexpr bool I8 = MODE == kModeI8;
   constexpr int kEB = I8 ? 1 : 2;   // bytes per element
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kPPLds];
+  // phase stamps: shader clock at entry, step 0 landed, K loop done, output
+  // staged in LDS, stores complete; 100 MHz clock at entry and at the end
+  unsigned long long st[5] = {0, 0, 0, 0, 0};
+  unsigned long long rt0 = 0;
+  if constexpr (STAMPS) {
+    __builtin_amdgcn_sched_barrier(0);
+    rt0 = __builtin_amdgcn_s_memrealtime();
+  }
+  LTX25_TSTAMP(st[0])
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -302,6 +323,7 @@ tall_kernel(TallParams p)
     LTX25_VMCNT(0);
   }
   __builtin_amdgcn_s_barrier();
+  LTX25_TSTAMP(st[1])
   if (g == 1) { __builtin_amdgcn_s_barrier(); }
 
   // ---- main loop. Group 0 runs M(s) in phase 2 s and C(s) in 2 s + 1, group
@@ -368,6 +390,7 @@ tall_kernel(TallParams p)
   }
   if (g == 0) { __builtin_amdgcn_s_barrier(); }
   __syncthreads();   // every wave is done reading the operand stages
+  LTX25_TSTAMP(st[2])
 
   // ---- epilogue. Accumulator block (i, j), lane l, register r (the MFMAs
   // take the weight fragment first): row 16 i + l % 16 of the wave's rows,
@@ -466,6 +489,7 @@ tall_kernel(TallParams p)
     }
   }
   __syncthreads();
+  LTX25_TSTAMP(st[3])
   constexpr int CPR = kBN / 8;   // 16-byte chunks per output row
 #pragma unroll 4
   for (int q = tid; q < kBM * CPR; q += kThreads) {
@@ -477,6 +501,23 @@ tall_kernel(TallParams p)
     const uint4 v = *(const uint4*)(stage + r * kEP + c);
     // non-temporal: the tile is not read again by this launch
     __builtin_nontemporal_store(__builtin_bit_cast(i32x4, v), (i32x4*)(p.y + (size_t)m * p.N + nn));
+  }
+  if constexpr (STAMPS) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the stores have completed
+    LTX25_TSTAMP(st[4])
+    const unsigned long long rt1 = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_sched_barrier(0);
+    if (p.stamps != nullptr && lane == 0) {
+      // HW_ID (CU, SH, SE of this wave) and XCC_ID, read from the hardware registers
+      const unsigned long long hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+      const unsigned long long xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);
+      unsigned long long* o = p.stamps + ((size_t)blockIdx.x * 8 + wave) * 8;
+#pragma unroll
+      for (int i = 0; i < 5; ++i) { o[i] = st[i]; }
+      o[5] = rt0;
+      o[6] = rt1;
+      o[7] = (xcc << 32) | hw;
+    }
   }
 }
 
@@ -767,7 +808,16 @@ constexpr size_t kFourGib = (size_t)1 << 32;
 hipError_t launch_tall(const TallParams& p, int mode, hipStream_t stream)
 {
   const dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
-  if (mode == kModeI8) {
+  if (p.stamps != nullptr) {
+    // the phase-stamp instantiations (ltx25_probe_tall_phases)
+    if (mode == kModeI8) {
+      hipLaunchKernelGGL((tall_kernel<kModeI8, false, true>), grid, dim3(kThreads), 0, stream, p);
+    } else if (mode == kModeBf16 && p.x2 == nullptr) {
+      hipLaunchKernelGGL((tall_kernel<kModeBf16, false, true>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+      return hipErrorInvalidValue;
+    }
+  } else if (mode == kModeI8) {
     hipLaunchKernelGGL((tall_kernel<kModeI8, false>), grid, dim3(kThreads), 0, stream, p);
   } else if (mode == kModeW8) {
     hipLaunchKernelGGL(tall_w8_kernel, grid, dim3(kThreads), 0, stream, p);
@@ -803,7 +853,7 @@ bool tall_w8_takes(const GemmDesc& d, const GemmPlan& plan)
          (size_t)(d.M + kBM) * d.K * 2 < kFourGib && (size_t)(d.N + kBN) * d.K < kFourGib;
 }
 
-hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream)
+hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream, unsigned long long* stamps)
 {
   if (d.bits == 8) {
     GemmPlan plan;
@@ -854,6 +904,7 @@ hipError_t launch_tall_dense(const GemmDesc& d, hipStream_t stream)
   p.epilogue = d.epilogue;
   p.tiles_m = (d.M + kBM - 1) / kBM;
   p.tiles_n = (d.N + kBN - 1) / kBN;
+  p.stamps = stamps;
   return launch_tall(p, kModeBf16, stream);
 }
 
@@ -866,7 +917,8 @@ bool tall_i8_takes(int M, int N, int K)
 
 hipError_t launch_tall_i8(const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
                           const void* bias, int bias_type, int epilogue, uint16_t* y,
-                          int32_t* acc, int M, int K, int N, hipStream_t stream)
+                          int32_t* acc, int M, int K, int N, hipStream_t stream,
+                          unsigned long long* stamps)
 {
   if (M < 1 || !tall_i8_takes(M, N, K) || (size_t)M * N * 2 >= kTwoGib) {
     return hipErrorInvalidValue;
@@ -887,6 +939,7 @@ hipError_t launch_tall_i8(const int8_t* xq, const float* sx, const int8_t* wq, c
   p.epilogue = epilogue;
   p.tiles_m = (M + kBM - 1) / kBM;
   p.tiles_n = (N + kBN - 1) / kBN;
+  p.stamps = stamps;
   return launch_tall(p, kModeI8, stream);
 }
 
