@@ -116,20 +116,6 @@ dequant_kernel(const uint8_t* codes, const uint16_t* scales,
   const uint16_t* srow = scales + (size_t)n * gcols;
   const uint16_t* qrow = qbias + (size_t)n * gcols;
   uint16_t* orow = out + (size_t)n * ldo;
-  // columns [K, ldo) of the row: tail row n (tail_cols of it, zeros past
-  // them), 8 columns per thread, strided by the block so any width is covered
-  for (int c = (int)threadIdx.x * 8; tail != nullptr && blockIdx.y == 0 && c < ldo - K;
-       c += kBlock * 8) {
-    const uint16_t* trow = tail + (size_t)n * tail_ld;
-    uint32_t w[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint32_t lo = c + 2 * t < tail_cols ? trow[c + 2 * t] : 0u;
-      const uint32_t hi = c + 2 * t + 1 < tail_cols ? trow[c + 2 * t + 1] : 0u;
-      w[t] = lo | (hi << 16);
-    }
-    *(uint4*)(orow + K + c) = make_uint4(w[0], w[1], w[2], w[3]);
-  }
   uint32_t v[kDeqRuns][2];
   float s[kDeqRuns], b[kDeqRuns];
 #pragma unroll
@@ -149,6 +135,30 @@ dequant_kernel(const uint8_t* codes, const uint16_t* scales,
       s[j] = bf16_to_f32(srow[g]);
       b[j] = bf16_to_f32(qrow[g]);
     }
+  }
+  // Columns [K, ldo) of the row: tail row n (tail_cols of it, zeros past
+  // them), 8 columns per thread, strided by the block so any width is
+  // covered. Loaded after the codes, so that both loads are in flight
+  // together; one 16-byte load where the 8 columns are whole and aligned.
+  for (int c = (int)threadIdx.x * 8; tail != nullptr && blockIdx.y == 0 && c < ldo - K;
+       c += kBlock * 8) {
+    const uint16_t* trow = tail + (size_t)n * tail_ld;
+    uint32_t w[4];
+    if (c + 8 <= tail_cols && ((uintptr_t)(trow + c) & 15u) == 0) {
+      const uint4 t4 = *(const uint4*)(trow + c);
+      w[0] = t4.x;
+      w[1] = t4.y;
+      w[2] = t4.z;
+      w[3] = t4.w;
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t lo = c + 2 * t < tail_cols ? trow[c + 2 * t] : 0u;
+        const uint32_t hi = c + 2 * t + 1 < tail_cols ? trow[c + 2 * t + 1] : 0u;
+        w[t] = lo | (hi << 16);
+      }
+    }
+    *(uint4*)(orow + K + c) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 #pragma unroll
   for (int j = 0; j < kDeqRuns; ++j) {
