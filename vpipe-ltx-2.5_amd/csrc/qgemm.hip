@@ -669,7 +669,12 @@ qgemm_kernel(KParams p)
   }
 }
 
-// Sum the split-K partials in split order, then bias, epilogue, bf16.
+// Sum the split-K partials in split order, then bias, epilogue, bf16. The
+// partials of up to kRedBatch splits, the bias and y_in are loaded before any
+// is summed, so a thread waits for one memory round trip per batch, not one
+// per split (a loop of dependent loads waited for each in turn).
+constexpr int kRedBatch = 8;
+
 __global__ void __launch_bounds__(256)
 splitk_reduce_kernel(const float* partial, int splits, const void* bias,
                      int bias_type, int epilogue, const uint16_t* y_in, uint16_t* y, int M,
@@ -680,17 +685,53 @@ splitk_reduce_kernel(const float* partial, int splits, const void* bias,
   if (i0 >= total) { return; }
   const size_t plane = total;
   if ((N & 3) == 0 && i0 + 4 <= total) {
-    f32x4 s = *(const f32x4*)(partial + i0);
-    for (int k = 1; k < splits; ++k) {
-      const f32x4 v = *(const f32x4*)(partial + (size_t)k * plane + i0);
-      s += v;
+    // No branch around a partial's load (the wait counting then serializes
+    // them): splits past the last re-read the last one, and are not added.
+    // The first batch is issued before the bias and y_in loads, whose
+    // branches on the bias type would otherwise be waited for first.
+    f32x4 v[kRedBatch];
+#pragma unroll
+    for (int j = 0; j < kRedBatch; ++j) {
+      v[j] = *(const f32x4*)(partial + (size_t)min(j, splits - 1) * plane + i0);
     }
+    // one branch per operand, its four loads inside it
     const int n = (int)(i0 % (size_t)N);
+    float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float yi[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (bias_type == kBiasF32) {
+      const float* const bf = (const float*)bias + n;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) { b4[t] = bf[t]; }
+    } else if (bias_type == kBiasBf16) {
+      const uint16_t* const bh = (const uint16_t*)bias + n;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) { b4[t] = bf16_to_f32(bh[t]); }
+    }
+    if (y_in != nullptr) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) { yi[t] = bf16_to_f32(y_in[i0 + t]); }
+    }
+    // the sum in split order: split 0, then + split 1, + split 2, ...
+    f32x4 s = v[0];
+#pragma unroll
+    for (int j = 1; j < kRedBatch; ++j) {
+      if (j < splits) { s += v[j]; }
+    }
+    for (int k0 = kRedBatch; k0 < splits; k0 += kRedBatch) {
+#pragma unroll
+      for (int j = 0; j < kRedBatch; ++j) {
+        v[j] = *(const f32x4*)(partial + (size_t)min(k0 + j, splits - 1) * plane + i0);
+      }
+#pragma unroll
+      for (int j = 0; j < kRedBatch; ++j) {
+        if (k0 + j < splits) { s += v[j]; }
+      }
+    }
     float o[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      float v = s[t] + load_bias(bias, bias_type, n + t);
-      if (y_in != nullptr) { v += bf16_to_f32(y_in[i0 + t]); }
+      float v = s[t] + b4[t];
+      if (y_in != nullptr) { v += yi[t]; }
       if (epilogue == kEpiGelu) { v = gelu_tanh(v); }
       o[t] = v;
     }
