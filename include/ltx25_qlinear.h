@@ -329,9 +329,15 @@ int ltx25_lora_route(const void* x, const void* a, const void* b, const void* y,
  * (src/ltx25-block-metal.cc:428-436,523-524,639-648; ff_in's GELU after
  * both, :645). Where ltx25_lora_fold_takes says so (the dequant-once arm
  * of a quantized weight: M >= LTX25_DEQUANT_ONCE_AUTO_MIN_M under AUTO)
- * the adapter is folded into the linear's GEMM as rank-rounded-to-64 more
- * K: y = epi([x | r] . [W | B]^T + bias), r = bf16(x . A^T), one rounding
- * to bf16 where the reference rounds the linear and the delta separately.
+ * the adapter is folded into the linear's own GEMM:
+ *   - w8 codes, rank % 8 == 0 up to 64, K % 128 == 0, a and b 16-byte
+ *     aligned: merged into the expanded weight, W' = bf16(dequant(W) +
+ *     B . A), then y = epi(x . W'^T + bias) at the linear's own K
+ *     ((x . A^T) . B^T = x . (B . A)^T); one rounding per weight element
+ *     and one of the output;
+ *   - otherwise as rank-rounded-to-64 more K: y = epi([x | r] . [W | B]^T
+ *     + bias), r = bf16(x . A^T), one rounding of the output;
+ * where the reference rounds the linear and the delta separately.
  * Elsewhere it runs ltx25_linear_q, ltx25_lora_add, then ltx25_gelu_tanh
  * for LTX25_EPI_GELU_TANH. a is bf16 [rank][K], b bf16 [N][rank];
  * rank 0 is a plain linear. */

@@ -56,6 +56,11 @@ SHAPES = [  # name, M, K, N, rank, the route AUTO takes
     # super blocks ahead (ranks up to 64) run past the column split's end
     ("r first: rank 16, ragged N", 640, 1024, 1000, 16, RF),
     ("r first: rank 64, N = 4104", 520, 256, 4104, 64, RF),
+    # more rows: r's GEMM covers the CUs with fewer K splits; ragged M, a rank that is not a
+    # multiple of 16, K that is not a multiple of 512
+    ("r first, 2085 rows: rank 40, K = 2624", 2085, 2624, 1024, 40, RF),
+    ("r first, 2112 rows: rank 8, K = 1088", 2112, 1088, 256, 8, RF),
+    ("r first, 2048 rows: rank 64, K = 4096", 2048, 4096, 512, 64, RF),
 ]
 
 
@@ -167,6 +172,7 @@ def test_lora_is_deterministic(pkg, dev):
 # the reference's caller scratch r ([M][rank]): the r-first route, and the GEMM pair at a
 # rank that is a multiple of 64, compute r into it instead of the library's scratch
 CALLER_R = [("r first: rank 40, ragged M", 777, 1024, 2048, 40, RF),
+            ("r first: rank 56, 2085 rows", 2085, 2624, 512, 56, RF),
             ("GEMM pair, rank 128, no padding", 300, 2048, 1024, 128, P)]
 
 

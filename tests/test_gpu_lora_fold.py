@@ -1,7 +1,8 @@
 """The linear with its adapter in one call (ltx25_linear_q_lora), through the
-C ABI: the adapter folded into the linear's GEMM as extra K where
-lora_fold_takes says so, the reference's sequence (linear, lora_add, GELU)
-elsewhere.
+C ABI: the adapter folded into the linear's GEMM where lora_fold_takes says
+so -- merged into the expanded weight (w8 codes, rank % 8 == 0 up to 64,
+K % 128 == 0, aligned A and B), else as extra K -- and the reference's
+sequence (linear, lora_add, GELU) elsewhere.
 
 The reference applies the adapter between the linear and the GELU
 (src/ltx25-block-metal.cc:639-648). Bars:
@@ -31,13 +32,20 @@ REL_L2_SEQ = 1e-2
 
 # name, M, K, N, rank, bits, group, bias, epilogue, dequant-once mode
 CASES = [
-    ("rank 32 padded to 64, f32 bias, GELU", 256, 512, 384, 32, 8, 64, "f32", 1, "on"),
-    ("rank 64, bf16 bias", 320, 1024, 1024, 64, 8, 64, "bf16", 0, "on"),
+    # merged into the expansion
+    ("merged: rank 32, f32 bias, GELU", 256, 512, 384, 32, 8, 64, "f32", 1, "on"),
+    ("merged: rank 64, bf16 bias", 320, 1024, 1024, 64, 8, 64, "bf16", 0, "on"),
+    ("merged: w8g32, rank 48, N = 520 (a partial row tile), GELU", 1024, 1024, 520, 48, 8, 32,
+     "bf16", 1, "on"),
+    # as extra K: w4 codes, a rank that is not a multiple of 8, rank > 64, K % 128 != 0
     ("w4g32, rank 100 padded to 128, N = 520, GELU", 300, 768, 520, 100, 4, 32, None, 1, "on"),
-    ("split K across the two parts (128 x 128 tile)", 256, 4096, 512, 32, 8, 64, "f32", 0, "on"),
+    ("split K across the two parts (128 x 128 tile), rank 36", 256, 4096, 512, 36, 8, 64, "f32",
+     0, "on"),
     ("rank 1", 192, 256, 256, 1, 8, 64, None, 0, "on"),
+    ("rank 96, K = 1088", 512, 1088, 256, 96, 8, 64, "f32", 1, "on"),
     ("256 x 256 tile at the dequant-once threshold", 4096, 1024, 8192, 32, 8, 64, "bf16", 1,
      "auto"),
+    ("rank 40, ragged M, K = 2624", 2085, 2624, 512, 40, 8, 64, "f32", 1, "on"),
     # the expansion's [W | B] tail (2112 columns) is wider than one 256-thread
     # block's 2048: written by the tail loop
     ("rank 2100, tail wider than one block", 1024, 256, 256, 2100, 8, 64, "f32", 0, "auto"),
@@ -121,16 +129,17 @@ def test_fold_against_oracle_and_sequence(pkg, dev, name, M, K, N, rank, bits, g
     assert orc.rel_l2(orc.bf16_to_f32(host_bits(plain)), got) > 1e-3, name
 
 
-def test_fold_a_not_16_byte_aligned(pkg, dev):
+@pytest.mark.parametrize("M,rank", [(256, 64), (2080, 48)])
+def test_fold_a_not_16_byte_aligned(pkg, dev, M, rank):
     """A as a view one element into its storage: the fold pads it first."""
-    M, K, N, rank = 256, 512, 256, 64
+    K, N = 512, 256
     pkg.set_dequant_once(pkg.DEQUANT_ONCE_ON)
     xb, qw, wb, ab, bb, bias = _operands(pkg, M, K, N, rank, 8, 64, None, 7)
     store = torch.empty((rank * K + 8,), dtype=torch.bfloat16, device="cuda")
     ad = store[1:1 + rank * K].view(rank, K)
     ad.copy_(dev_bf16(ab))
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    say("lora fold with a misaligned A")
+    say(f"lora fold with a misaligned A, M={M} rank={rank}")
     pkg.linear_q_lora(dev_bf16(xb), qw, None, ad, dev_bf16(bb), rank, y, M, K, N)
     torch.cuda.synchronize()
     got = orc.bf16_to_f32(host_bits(y))

@@ -598,12 +598,18 @@ int lora_pair(DeviceState* ds, hipStream_t st, const void* x, const void* a, con
 // linear + lora_add round twice (src/ltx25-metal-ops.cc:940-1004); before
 // the GELU, as the reference applies the adapter
 // (src/ltx25-block-metal.cc:639-648).
+// Adapters up to rank 64 on w8 codes are merged into the expansion instead
+// (ltx25::launch_dequant_merge): W' = bf16(W + B . A), then the linear runs
+// at its own K over W'. (x . A^T) . B^T = x . (B . A)^T, so no r GEMM and no
+// extra K; one rounding per weight element and one of the output.
 struct FoldPlan {
   bool takes = false;
   int rk = 0;
   int bits = 0;
+  bool merge = false;        // the shape allows the merge (pointers checked at run time)
   ltx25::GemmPlan r_plan;
   ltx25::GemmPlan plan;
+  ltx25::GemmPlan merge_plan;   // the linear over W' [N][K]
 };
 
 FoldPlan plan_fold(int M, int K, int N, int rank, int bits, int cu_count, const void* x,
@@ -632,6 +638,13 @@ FoldPlan plan_fold(int M, int K, int N, int rank, int bits, int cu_count, const 
   f.plan = ltx25::plan_gemm(M, N, kt, 16, cu_count, tile);
   if (f.plan.tile == 2) { return f; }
   f.r_plan = ltx25::plan_gemm(M, rk, K, 16, cu_count);
+  // the merge's shape rule (A's and B's alignment and the group size are
+  // checked at run time)
+  f.merge = ltx25::dequant_merge_takes(bits, N, K, rank, nullptr, nullptr);
+  if (f.merge) {
+    f.merge_plan = ltx25::plan_gemm(M, N, K, 16, cu_count, tile);
+    f.merge = f.merge_plan.tile != 2;
+  }
   f.rk = rk;
   f.bits = bits;
   f.takes = true;
@@ -642,6 +655,41 @@ int run_fold(DeviceState* ds, hipStream_t st, const FoldPlan& f, const void* x,
              const ltx25_qweight* w, const void* bias, int bias_dtype, const void* a,
              const void* b, int rank, void* y, int M, int K, int N, int epilogue)
 {
+  if (f.merge && aligned16(a) && aligned16(b) && (w->group == 32 || w->group == 64)) {
+    // W' = bf16(W + B . A), then y = epi(x . W'^T + bias)
+    uint16_t* wd = nullptr;
+    float* ws = nullptr;
+    {
+      std::lock_guard<std::mutex> lk(g_mu);
+      int rc = grow(&ds->deq, &ds->deq_bytes, (size_t)N * K * 2);
+      if (rc != LTX25_OK) { return rc; }
+      if (f.merge_plan.workspace_bytes > 0) {
+        rc = grow(&ds->ws, &ds->ws_bytes, f.merge_plan.workspace_bytes);
+        if (rc != LTX25_OK) { return rc; }
+        ws = (float*)ds->ws;
+      }
+      wd = (uint16_t*)ds->deq;
+    }
+    hipError_t e = ltx25::launch_dequant_merge(
+        (const uint8_t*)w->codes, (const uint16_t*)w->scales, (const uint16_t*)w->qbias,
+        w->group, (const uint16_t*)a, (const uint16_t*)b, rank, wd, N, K, st);
+    if (e != hipSuccess) { return hip_fail(e, "fold: merge launch"); }
+    ltx25::GemmDesc d;
+    d.x = (const uint16_t*)x;
+    d.w = wd;
+    d.bits = 16;
+    d.group = 64;
+    d.bias = bias;
+    d.bias_type = bias != nullptr ? bias_dtype : ltx25::kBiasNone;
+    d.epilogue = epilogue;
+    d.y = (uint16_t*)y;
+    d.M = M;
+    d.N = N;
+    d.K = K;
+    e = ltx25::launch_gemm(d, f.merge_plan, ws, st);
+    if (e != hipSuccess) { return hip_fail(e, "fold: gemm launch"); }
+    return LTX25_OK;
+  }
   const int rk = f.rk;
   const int kt = K + rk;
   // A [rank][K] is read as an [rk][K] weight whose rows past `rank` are

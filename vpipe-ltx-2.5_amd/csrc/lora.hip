@@ -414,7 +414,174 @@ __global__ void lora_pad_kernel(const uint16_t* __restrict__ src, int rows, int 
   *(uint4*)(dst + r * (size_t)ld_dst + c) = v;
 }
 
+// ---- the adapter merged into the dequant-once expansion ----------------
+//   W'[n][k] = bf16(fma(scale, code, bias) + sum_{i < rank} B[n][i] A[i][k])
+// The linear then runs over W' at its own K. (x . A^T) . B^T = x . (B . A)^T,
+// so this is the adapter of the reference's lora_add
+// (src/ltx25-metal-ops.cc:989-1004) applied to the weight instead of the
+// output: no r GEMM, and no extra K in the linear. One rounding to bf16 per
+// weight element, where the reference rounds r = x . A^T and the output.
+//
+// One workgroup expands kMgTiles tiles of 64 rows x 128 columns of W (w8
+// codes), stacked along N:
+//   1. A's columns k0..k0+127 (rank rows, zero rows up to R) are staged
+//      transposed in LDS once, so each MFMA fragment of A is one 16-byte
+//      read;
+//   2. per tile, wave w owns rows 16 w..16 w+15: D = B[rows][0..R) .
+//      A[0..R)[k0..k0+127] on v_mfma_f32_16x16x32_bf16 (B's fragment
+//      first, eight 16-column blocks, R / 32 MFMAs each) goes to the wave's
+//      own LDS rows as f32;
+//   3. the wave reads its rows back as runs of 8, dequantizes four runs per
+//      lane, adds D and rounds once: one 16-byte store per run.
+// Each wave reads back only what it wrote, so the tiles need no barrier.
+// The next tile's codes, scales, zero points and B fragments are loaded
+// before the current tile's MFMAs; the tiles are unrolled, so every wait
+// is exact (a loop around register-carried loads makes the compiler wait
+// for all of them at its head).
+constexpr int kMgRows = 64;
+constexpr int kMgCols = 128;
+constexpr int kMgTiles = 4;
+constexpr int kMgThreads = 256;
+constexpr int kMgRuns = 16 * kMgCols / 8 / 64;   // runs of 8 per lane per tile: 4
+constexpr int kMgDp = kMgCols + 4;               // f32 per LDS row of D
+
+template <int R>   // rank rounded up to 32 or 64
+__global__ __launch_bounds__(kMgThreads) void dequant_merge_kernel(
+    const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ qbias, int gshift, int gcols, const uint16_t* __restrict__ a,
+    const uint16_t* __restrict__ b, int rank, uint16_t* __restrict__ out, int N, int K)
+{
+  constexpr int AP = R + 8;   // bf16 per LDS row of A^T (16-byte pad keeps rows aligned)
+  __shared__ __attribute__((aligned(16))) float dl[kMgRows * kMgDp];
+  __shared__ __attribute__((aligned(16))) uint16_t at[kMgCols * AP];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int k0 = blockIdx.x * kMgCols;
+  const int nb = blockIdx.y * kMgRows * kMgTiles + 16 * wave;   // the wave's first row, tile 0
+  float* const dw = dl + 16 * wave * kMgDp;                      // the wave's 16 rows of D
+  const auto rb = rsrc(b, (size_t)N * rank * 2);
+
+  // run j of a lane in a tile: the wave's row rr, columns cc .. cc + 7
+  auto run_row = [&](int j) { return (lane + 64 * j) / (kMgCols / 8); };
+  auto run_col = [&](int j) { return ((lane + 64 * j) % (kMgCols / 8)) * 8; };
+  uint2 cv[2][kMgRuns];
+  float sv[2][kMgRuns], bv[2][kMgRuns];
+  i32x4 bf[2][R / 32];
+  auto load_tile = [&](int buf, int tt) {
+    const int n_w = nb + tt * kMgRows;
+#pragma unroll
+    for (int j = 0; j < kMgRuns; ++j) {
+      const int n = n_w + run_row(j);
+      const int nc = n < N ? n : N - 1;
+      const int k = k0 + run_col(j);
+      cv[buf][j] = *(const uint2*)(codes + (size_t)nc * K + k);
+      const int g = k >> gshift;
+      sv[buf][j] = bf16_to_f32(scales[(size_t)nc * gcols + g]);
+      bv[buf][j] = bf16_to_f32(qbias[(size_t)nc * gcols + g]);
+    }
+    // B's fragment: row n_w + lane % 16, adapter columns 32 c + 8 (lane / 16) .. + 7
+    const int n = n_w + (lane & 15);
+#pragma unroll
+    for (int c = 0; c < R / 32; ++c) {
+      const int i = 32 * c + 8 * (lane >> 4);
+      const uint32_t off = (n < N && i < rank) ? (uint32_t)(n * rank + i) * 2u : kOob;
+      bf[buf][c] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)off, 0, 0);
+    }
+  };
+  load_tile(0, 0);
+
+  // 1. at[kk][i] = A[i][k0 + kk], zero for i >= rank
+  const auto ra = rsrc(a, (size_t)rank * K * 2);
+  for (int p = tid; p < R * (kMgCols / 8); p += kMgThreads) {
+    const int i = p / (kMgCols / 8);
+    const int kk = (p % (kMgCols / 8)) * 8;
+    const uint32_t off = i < rank ? (uint32_t)(i * K + k0 + kk) * 2u : kOob;
+    const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)off, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      at[(kk + 2 * e) * AP + i] = (uint16_t)((uint32_t)v[e] & 0xffffu);
+      at[(kk + 2 * e + 1) * AP + i] = (uint16_t)((uint32_t)v[e] >> 16);
+    }
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int tt = 0; tt < kMgTiles; ++tt) {
+    const int cur = tt & 1;
+    if (tt + 1 < kMgTiles) { load_tile(cur ^ 1, tt + 1); }
+    // 2. D[4 (lane / 16) + t][16 kb + lane % 16] of the wave's rows
+#pragma unroll
+    for (int kb = 0; kb < kMgCols / 16; ++kb) {
+      f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < R / 32; ++c) {
+        const i32x4 af = *(const i32x4*)(at + (16 * kb + (lane & 15)) * AP + 32 * c +
+                                         8 * (lane >> 4));
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, bf[cur][c]),
+                                                    __builtin_bit_cast(bf16x8, af), d, 0, 0, 0);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        dw[(4 * (lane >> 4) + t) * kMgDp + 16 * kb + (lane & 15)] = d[t];
+      }
+    }
+    // 3. W' = bf16(fma(s, code, z) + D), one 16-byte store per run
+    const int n_w = nb + tt * kMgRows;
+#pragma unroll
+    for (int j = 0; j < kMgRuns; ++j) {
+      const int rr = run_row(j);
+      const int cc = run_col(j);
+      const f32x4 d0 = *(const f32x4*)(dw + rr * kMgDp + cc);
+      const f32x4 d1 = *(const f32x4*)(dw + rr * kMgDp + cc + 4);
+      const float dd[8] = {d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3]};
+      uint32_t o[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const uint32_t w = h < 2 ? cv[cur][j].x : cv[cur][j].y;
+        const int sh = (h & 1) * 16;
+        o[h] = pack_bf16x2(fmaf(sv[cur][j], (float)((w >> sh) & 0xffu), bv[cur][j]) + dd[2 * h],
+                           fmaf(sv[cur][j], (float)((w >> (sh + 8)) & 0xffu), bv[cur][j]) +
+                               dd[2 * h + 1]);
+      }
+      const int n = n_w + rr;
+      if (n < N) { *(uint4*)(out + (size_t)n * K + k0 + cc) = make_uint4(o[0], o[1], o[2], o[3]); }
+    }
+  }
+}
+
 }  // namespace
+
+// The merge takes w8 codes, K % 128 == 0, rank % 8 == 0 up to 64, A and B
+// 16-byte aligned and every operand under 2 GiB (32-bit buffer offsets).
+bool dequant_merge_takes(int bits, int N, int K, int rank, const void* a, const void* b)
+{
+  const size_t lim = (size_t)1 << 31;
+  return bits == 8 && N > 0 && K > 0 && K % kMgCols == 0 && rank > 0 && rank <= 64 &&
+         rank % 8 == 0 && ((uintptr_t)a & 15u) == 0 && ((uintptr_t)b & 15u) == 0 &&
+         (size_t)rank * K * 2 < lim && (size_t)N * rank * 2 < lim && (size_t)N * K * 2 < lim;
+}
+
+hipError_t launch_dequant_merge(const uint8_t* codes, const uint16_t* scales,
+                                const uint16_t* qbias, int group, const uint16_t* a,
+                                const uint16_t* b, int rank, uint16_t* out, int N, int K,
+                                hipStream_t stream)
+{
+  if (!dequant_merge_takes(8, N, K, rank, a, b) || (group != 32 && group != 64)) {
+    return hipErrorInvalidValue;
+  }
+  const int gshift = group == 64 ? 6 : 5;
+  const int rows = kMgRows * kMgTiles;
+  const dim3 grid((unsigned)(K / kMgCols), (unsigned)((N + rows - 1) / rows));
+  if (rank <= 32) {
+    dequant_merge_kernel<32><<<grid, kMgThreads, 0, stream>>>(codes, scales, qbias, gshift,
+                                                              K / group, a, b, rank, out, N, K);
+  } else {
+    dequant_merge_kernel<64><<<grid, kMgThreads, 0, stream>>>(codes, scales, qbias, gshift,
+                                                              K / group, a, b, rank, out, N, K);
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_lora_pad(const uint16_t* src, int rows, int cols, int ld_src, uint16_t* dst,
                            int ld_dst, hipStream_t stream, int width)
