@@ -481,29 +481,48 @@ tall_kernel(TallParams p)
       }
     }
   }
+  // The epilogue's choices are made once, outside the unrolled staging loop:
+  // a runtime test per output became a scalar branch per output, which kept
+  // the scheduler from interleaving outputs (and made it rematerialize the
+  // GELU's constants per output). Without a bias the add of +0 is skipped:
+  // an accumulator is never -0 (it starts at +0, or at y_in, and x + (-x)
+  // rounds to +0), so the bits are the same.
+  auto stage_tile = [&](auto gelu, auto biased) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int c = wn * 64 + j * 16 + lcol;
+    for (int j = 0; j < 4; ++j) {
+      const int c = wn * 64 + j * 16 + lcol;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = g * 128 + i * 16 + lrow;
-      float v[4];
-      if constexpr (I8) {
+      for (int i = 0; i < 8; ++i) {
+        const int r = g * 128 + i * 16 + lrow;
+        float v[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          // y = bf16(fma(float(acc), sx[m] * sw[n], bias[n])), that order
-          v[t] = fmaf((float)acc[i][j][t], sxm[i] * sw4s[j][t], b4s[j][t]);
+          if constexpr (I8) {
+            // y = bf16(fma(float(acc), sx[m] * sw[n], bias[n])), that order
+            v[t] = fmaf((float)acc[i][j][t], sxm[i] * sw4s[j][t], b4s[j][t]);
+          } else if constexpr (decltype(biased)::value) {
+            v[t] = acc[i][j][t] + b4s[j][t];
+          } else {
+            v[t] = acc[i][j][t];
+          }
+          if constexpr (decltype(gelu)::value) { v[t] = gelu_tanh(v[t]); }
         }
-      } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) { v[t] = acc[i][j][t] + b4s[j][t]; }
+        *(uint2*)(stage + r * kEP + c) =
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (p.epilogue == kEpiGelu) { v[t] = gelu_tanh(v[t]); }
-      }
-      *(uint2*)(stage + r * kEP + c) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     }
+  };
+  const bool biased = p.bias_type != kBiasNone;
+  if (p.epilogue == kEpiGelu) {
+    if (biased) {
+      stage_tile(std::true_type{}, std::true_type{});
+    } else {
+      stage_tile(std::true_type{}, std::false_type{});
+    }
+  } else if (biased) {
+    stage_tile(std::false_type{}, std::true_type{});
+  } else {
+    stage_tile(std::false_type{}, std::false_type{});
   }
   __syncthreads();
   LTX25_TSTAMP(st[3])
@@ -789,21 +808,30 @@ tall_w8_kernel(TallParams p)
   const int lrow = lane & 15;
   const int lcol = (lane >> 4) * 4;
   uint16_t* const stage = lds;
+  // the GELU choice made once, outside the unrolled staging loop
+  auto stage_tile = [&](auto gelu) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int c = wn * 64 + j * 16 + lcol;
-    const f32x4 b4 = *(const f32x4*)pad_at(480, c);
+    for (int j = 0; j < 4; ++j) {
+      const int c = wn * 64 + j * 16 + lcol;
+      const f32x4 b4 = *(const f32x4*)pad_at(480, c);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = wm * 128 + i * 16 + lrow;
-      float v[4];
+      for (int i = 0; i < 8; ++i) {
+        const int r = wm * 128 + i * 16 + lrow;
+        float v[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        v[t] = acc[i][j][t] + b4[t];
-        if (p.epilogue == kEpiGelu) { v[t] = gelu_tanh(v[t]); }
+        for (int t = 0; t < 4; ++t) {
+          v[t] = acc[i][j][t] + b4[t];
+          if constexpr (decltype(gelu)::value) { v[t] = gelu_tanh(v[t]); }
+        }
+        *(uint2*)(stage + r * kEP + c) =
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }
-      *(uint2*)(stage + r * kEP + c) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     }
+  };
+  if (p.epilogue == kEpiGelu) {
+    stage_tile(std::true_type{});
+  } else {
+    stage_tile(std::false_type{});
   }
   __syncthreads();
   constexpr int CPR = kBN / 8;
