@@ -217,3 +217,41 @@ def test_fold_at_the_ffn_shape(pkg, dev):
                             bias.cpu().numpy(), 1, np.arange(len(rows)))
     assert orc.max_rel(got, ref_rows) <= MAX_REL
     assert orc.rel_l2(got, ref_rows) < REL_L2_ORACLE
+
+
+def _sweep_draw(i):
+    """A seeded random fold shape: both forms (merged: w8, rank % 8 == 0 up to 64,
+    K % 128 == 0; extra K otherwise), ragged M and N, groups of 64 and 32, every bias kind,
+    with and without GELU, the dequant-once arm forced on so the fold takes."""
+    rng = np.random.default_rng(7000 + i)
+    bits, group = [(8, 64), (8, 32), (8, 64), (4, 64), (8, 32)][i % 5]
+    M = int(rng.choice([130, 256, 333, 512, 700]))
+    K = 64 * int(rng.integers(1, 33))
+    N = int(rng.choice([64, 200, 384, 520, 1000, 2050]))
+    N = max(8, N - N % 8)
+    rank = int(rng.choice([1, 8, 12, 16, 24, 32, 40, 48, 56, 64, 72, 96]))
+    bias = [None, "bf16", "f32"][int(rng.integers(0, 3))]
+    epi = int(rng.integers(0, 2))
+    return M, K, N, rank, bits, group, bias, epi
+
+
+SWEEP = [_sweep_draw(i) for i in range(20)]
+
+
+@pytest.mark.parametrize("M,K,N,rank,bits,group,bias_kind,epi", SWEEP,
+                         ids=[f"s{i}" for i in range(len(SWEEP))])
+def test_fold_random_shapes(pkg, dev, M, K, N, rank, bits, group, bias_kind, epi):
+    pkg.set_dequant_once(pkg.DEQUANT_ONCE_ON)
+    assert pkg.lora_fold_takes(M, K, N, rank, bits)
+    xb, qw, wb, ab, bb, bias = _operands(pkg, M, K, N, rank, bits, group, bias_kind,
+                                         M * 7 + K + N + rank)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    say(f"lora fold sweep: M={M} K={K} N={N} rank={rank} w{bits}g{group} bias={bias_kind} "
+        f"epi={epi}")
+    pkg.linear_q_lora(dev_bf16(xb), qw, _bias_dev(bias, bias_kind), dev_bf16(ab), dev_bf16(bb),
+                      rank, y, M, K, N, epi)
+    torch.cuda.synchronize()
+    got = orc.bf16_to_f32(host_bits(y))
+    ref = _oracle_rows(xb, wb, ab, bb, bias, epi, np.arange(M))
+    assert orc.max_rel(got, ref) <= MAX_REL
+    assert orc.rel_l2(got, ref) < REL_L2_ORACLE
