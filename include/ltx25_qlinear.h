@@ -330,9 +330,9 @@ int ltx25_lora_route(const void* x, const void* a, const void* b, const void* y,
  * both, :645). Where ltx25_lora_fold_takes says so (the dequant-once arm
  * of a quantized weight: M >= LTX25_DEQUANT_ONCE_AUTO_MIN_M under AUTO)
  * the adapter is folded into the linear's own GEMM:
- *   - w8 codes, rank % 8 == 0 up to 64, K % 128 == 0, a and b 16-byte
- *     aligned: merged into the expanded weight, W' = bf16(dequant(W) +
- *     B . A), then y = epi(x . W'^T + bias) at the linear's own K
+ *   - w8 codes, rank up to 64, K % 128 == 0, a 16-byte aligned: merged
+ *     into the expanded weight, W' = bf16(dequant(W) + B . A), then
+ *     y = epi(x . W'^T + bias) at the linear's own K
  *     ((x . A^T) . B^T = x . (B . A)^T); one rounding per weight element
  *     and one of the output;
  *   - otherwise as rank-rounded-to-64 more K: y = epi([x | r] . [W | B]^T

@@ -1,8 +1,8 @@
 """The linear with its adapter in one call (ltx25_linear_q_lora), through the
 C ABI: the adapter folded into the linear's GEMM where lora_fold_takes says
-so -- merged into the expanded weight (w8 codes, rank % 8 == 0 up to 64,
-K % 128 == 0, aligned A and B), else as extra K -- and the reference's
-sequence (linear, lora_add, GELU) elsewhere.
+so -- merged into the expanded weight (w8 codes, K % 128 == 0, aligned A,
+rank up to 64), else as extra K -- and the reference's sequence (linear,
+lora_add, GELU) elsewhere.
 
 The reference applies the adapter between the linear and the GELU
 (src/ltx25-block-metal.cc:639-648). Bars:
@@ -37,7 +37,12 @@ CASES = [
     ("merged: rank 64, bf16 bias", 320, 1024, 1024, 64, 8, 64, "bf16", 0, "on"),
     ("merged: w8g32, rank 48, N = 520 (a partial row tile), GELU", 1024, 1024, 520, 48, 8, 32,
      "bf16", 1, "on"),
-    # as extra K: w4 codes, a rank that is not a multiple of 8, rank > 64, K % 128 != 0
+    # B copied with its rank padded to a multiple of 8
+    ("merged: rank 36 (B padded to 40)", 1024, 512, 256, 36, 8, 64, "f32", 0, "on"),
+    # as extra K: w4 codes, rank above 64, an unaligned A, K % 128 != 0
+    ("rank 128, f32 bias", 1024, 512, 256, 128, 8, 64, "f32", 0, "on"),
+    ("w8g32, rank 200, GELU", 1024, 1024, 512, 200, 8, 32, "bf16", 1, "on"),
+    ("rank 450, N = 520, GELU", 1024, 512, 520, 450, 8, 64, None, 1, "on"),
     ("w4g32, rank 100 padded to 128, N = 520, GELU", 300, 768, 520, 100, 4, 32, None, 1, "on"),
     ("split K across the two parts (128 x 128 tile), rank 36", 256, 4096, 512, 36, 8, 64, "f32",
      0, "on"),
@@ -220,7 +225,7 @@ def test_fold_at_the_ffn_shape(pkg, dev):
 
 
 def _sweep_draw(i):
-    """A seeded random fold shape: both forms (merged: w8, rank % 8 == 0 up to 64,
+    """A seeded random fold shape: both forms (merged: w8, rank up to 64,
     K % 128 == 0; extra K otherwise), ragged M and N, groups of 64 and 32, every bias kind,
     with and without GELU, the dequant-once arm forced on so the fold takes."""
     rng = np.random.default_rng(7000 + i)

@@ -598,10 +598,12 @@ int lora_pair(DeviceState* ds, hipStream_t st, const void* x, const void* a, con
 // linear + lora_add round twice (src/ltx25-metal-ops.cc:940-1004); before
 // the GELU, as the reference applies the adapter
 // (src/ltx25-block-metal.cc:639-648).
-// Adapters up to rank 64 on w8 codes are merged into the expansion instead
+// On w8 codes the adapter is merged into the expansion instead
 // (ltx25::launch_dequant_merge): W' = bf16(W + B . A), then the linear runs
 // at its own K over W'. (x . A^T) . B^T = x . (B . A)^T, so no r GEMM and no
-// extra K; one rounding per weight element and one of the output.
+// extra K; one rounding per weight element and one of the output. Taken up
+// to rank 64 (kMergeMaxRank): above it the merge kernel is LDS-bound and
+// the extra K costs less.
 struct FoldPlan {
   bool takes = false;
   int rk = 0;
@@ -638,9 +640,9 @@ FoldPlan plan_fold(int M, int K, int N, int rank, int bits, int cu_count, const 
   f.plan = ltx25::plan_gemm(M, N, kt, 16, cu_count, tile);
   if (f.plan.tile == 2) { return f; }
   f.r_plan = ltx25::plan_gemm(M, rk, K, 16, cu_count);
-  // the merge's shape rule (A's and B's alignment and the group size are
-  // checked at run time)
-  f.merge = ltx25::dequant_merge_takes(bits, N, K, rank, nullptr, nullptr);
+  // the merge's shape rule (A's alignment and the group size are checked
+  // at run time; B is copied with its rank padded to 8 when it needs to be)
+  f.merge = ltx25::dequant_merge_takes(bits, N, K, rank, (rank + 7) & ~7, nullptr, nullptr);
   if (f.merge) {
     f.merge_plan = ltx25::plan_gemm(M, N, K, 16, cu_count, tile);
     f.merge = f.merge_plan.tile != 2;
@@ -655,14 +657,24 @@ int run_fold(DeviceState* ds, hipStream_t st, const FoldPlan& f, const void* x,
              const ltx25_qweight* w, const void* bias, int bias_dtype, const void* a,
              const void* b, int rank, void* y, int M, int K, int N, int epilogue)
 {
-  if (f.merge && aligned16(a) && aligned16(b) && (w->group == 32 || w->group == 64)) {
-    // W' = bf16(W + B . A), then y = epi(x . W'^T + bias)
+  if (f.merge && aligned16(a) && (w->group == 32 || w->group == 64)) {
+    // W' = bf16(W + B . A), then y = epi(x . W'^T + bias); B is copied with
+    // its rank padded to a multiple of 8 (zero columns) when its rows are not
+    // whole 16-byte pieces
+    const int rank8 = (rank + 7) & ~7;
+    const bool pad_b = rank8 != rank || !aligned16(b);
     uint16_t* wd = nullptr;
+    uint16_t* bp = nullptr;
     float* ws = nullptr;
     {
       std::lock_guard<std::mutex> lk(g_mu);
       int rc = grow(&ds->deq, &ds->deq_bytes, (size_t)N * K * 2);
       if (rc != LTX25_OK) { return rc; }
+      if (pad_b) {
+        rc = grow(&ds->lora_mm, &ds->lora_mm_bytes, (size_t)N * rank8 * 2);
+        if (rc != LTX25_OK) { return rc; }
+        bp = (uint16_t*)ds->lora_mm;
+      }
       if (f.merge_plan.workspace_bytes > 0) {
         rc = grow(&ds->ws, &ds->ws_bytes, f.merge_plan.workspace_bytes);
         if (rc != LTX25_OK) { return rc; }
@@ -670,9 +682,15 @@ int run_fold(DeviceState* ds, hipStream_t st, const FoldPlan& f, const void* x,
       }
       wd = (uint16_t*)ds->deq;
     }
-    hipError_t e = ltx25::launch_dequant_merge(
+    hipError_t e = hipSuccess;
+    if (pad_b) {
+      e = ltx25::launch_lora_pad((const uint16_t*)b, N, rank, rank, bp, rank8, st);
+      if (e != hipSuccess) { return hip_fail(e, "fold: B pad launch"); }
+    }
+    e = ltx25::launch_dequant_merge(
         (const uint8_t*)w->codes, (const uint16_t*)w->scales, (const uint16_t*)w->qbias,
-        w->group, (const uint16_t*)a, (const uint16_t*)b, rank, wd, N, K, st);
+        w->group, (const uint16_t*)a, pad_b ? bp : (const uint16_t*)b, rank,
+        pad_b ? rank8 : rank, wd, N, K, st);
     if (e != hipSuccess) { return hip_fail(e, "fold: merge launch"); }
     ltx25::GemmDesc d;
     d.x = (const uint16_t*)x;

@@ -197,14 +197,16 @@ hipError_t launch_lora_pad(const uint16_t* src, int rows, int cols, int ld_src, 
                            int ld_dst, hipStream_t stream, int width = 0);
 // The dequant-once expansion with the adapter merged in (lora.hip):
 // out [N][K] = bf16(fma(scale, code, zero point) + B . A), A bf16
-// [rank][K], B bf16 [N][rank]. dequant_merge_takes: w8 codes, K % 128 == 0,
-// rank % 8 == 0 and at most 64, A and B 16-byte aligned, operands under
-// 2 GiB; launch_dequant_merge refuses anything else (groups of 32 or 64).
-bool dequant_merge_takes(int bits, int N, int K, int rank, const void* a, const void* b);
+// [rank][K], B bf16 [N][ldb] (columns from rank to ldb zero).
+// dequant_merge_takes: w8 codes, K % 128 == 0, rank at most kMergeMaxRank,
+// ldb a multiple of 8, A and B 16-byte aligned, operands under 2 GiB;
+// launch_dequant_merge refuses anything else (groups of 32 or 64).
+constexpr int kMergeMaxRank = 64;
+bool dequant_merge_takes(int bits, int N, int K, int rank, int ldb, const void* a, const void* b);
 hipError_t launch_dequant_merge(const uint8_t* codes, const uint16_t* scales,
                                 const uint16_t* qbias, int group, const uint16_t* a,
-                                const uint16_t* b, int rank, uint16_t* out, int N, int K,
-                                hipStream_t stream);
+                                const uint16_t* b, int rank, int ldb, uint16_t* out, int N,
+                                int K, hipStream_t stream);
 
 hipError_t launch_bias_add(uint16_t* y, const void* bias, int bias_type,
                            int M, int N, hipStream_t stream);

@@ -30,6 +30,8 @@
 // of a row block) and the kernel runs phase 2 only, reading its 32 rows of
 // r from that buffer (`r_in`, [M][rank], rank % 8 == 0).
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace ltx25 {
@@ -444,12 +446,17 @@ constexpr int kMgTiles = 4;
 constexpr int kMgThreads = 256;
 constexpr int kMgRuns = 16 * kMgCols / 8 / 64;   // runs of 8 per lane per tile: 4
 constexpr int kMgDp = kMgCols + 4;               // f32 per LDS row of D
+constexpr int kMgMaxRank = kMergeMaxRank;         // the widest instantiation
 
-template <int R>   // rank rounded up to 32 or 64
+// R: the rank rounded up to 32 or 64. Wider adapters would re-read a wider
+// transposed A slice from LDS for every 16 rows of W: at R = 480 the kernel
+// took 253 us at the FFN up shape, LDS-bound, where the extra-K fold costs
+// 155 us, so the host takes the merge up to rank 64 only.
+template <int R>
 __global__ __launch_bounds__(kMgThreads) void dequant_merge_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ qbias, int gshift, int gcols, const uint16_t* __restrict__ a,
-    const uint16_t* __restrict__ b, int rank, uint16_t* __restrict__ out, int N, int K)
+    const uint16_t* __restrict__ b, int rank, int ldb, uint16_t* __restrict__ out, int N, int K)
 {
   constexpr int AP = R + 8;   // bf16 per LDS row of A^T (16-byte pad keeps rows aligned)
   __shared__ __attribute__((aligned(16))) float dl[kMgRows * kMgDp];
@@ -460,7 +467,7 @@ __global__ __launch_bounds__(kMgThreads) void dequant_merge_kernel(
   const int k0 = blockIdx.x * kMgCols;
   const int nb = blockIdx.y * kMgRows * kMgTiles + 16 * wave;   // the wave's first row, tile 0
   float* const dw = dl + 16 * wave * kMgDp;                      // the wave's 16 rows of D
-  const auto rb = rsrc(b, (size_t)N * rank * 2);
+  const auto rb = rsrc(b, (size_t)N * ldb * 2);
 
   // run j of a lane in a tile: the wave's row rr, columns cc .. cc + 7
   auto run_row = [&](int j) { return (lane + 64 * j) / (kMgCols / 8); };
@@ -481,27 +488,45 @@ __global__ __launch_bounds__(kMgThreads) void dequant_merge_kernel(
       bv[buf][j] = bf16_to_f32(qbias[(size_t)nc * gcols + g]);
     }
     // B's fragment: row n_w + lane % 16, adapter columns 32 c + 8 (lane / 16) .. + 7
+    // (B's columns from rank up to ldb are zeros)
     const int n = n_w + (lane & 15);
 #pragma unroll
     for (int c = 0; c < R / 32; ++c) {
       const int i = 32 * c + 8 * (lane >> 4);
-      const uint32_t off = (n < N && i < rank) ? (uint32_t)(n * rank + i) * 2u : kOob;
+      const uint32_t off = (n < N && i < rank) ? (uint32_t)(n * ldb + i) * 2u : kOob;
       bf[buf][c] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)off, 0, 0);
     }
   };
   load_tile(0, 0);
 
-  // 1. at[kk][i] = A[i][k0 + kk], zero for i >= rank
+  // 1. at[kk][i] = A[i][k0 + kk], zero for i >= rank: R / 16 pieces of 16
+  // bytes per thread, loaded in batches of up to 8 before any is written (a
+  // load-then-write loop waited for each load in turn)
   const auto ra = rsrc(a, (size_t)rank * K * 2);
-  for (int p = tid; p < R * (kMgCols / 8); p += kMgThreads) {
-    const int i = p / (kMgCols / 8);
-    const int kk = (p % (kMgCols / 8)) * 8;
-    const uint32_t off = i < rank ? (uint32_t)(i * K + k0 + kk) * 2u : kOob;
-    const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)off, 0, 0);
+  constexpr int kPieces = R * (kMgCols / 8) / kMgThreads;
+  constexpr int kBatch = kPieces % 8 == 0 ? 8 : kPieces % 6 == 0 ? 6 : kPieces < 8 ? kPieces : 1;
+  static_assert(kPieces % kBatch == 0, "whole batches of A pieces");
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      at[(kk + 2 * e) * AP + i] = (uint16_t)((uint32_t)v[e] & 0xffffu);
-      at[(kk + 2 * e + 1) * AP + i] = (uint16_t)((uint32_t)v[e] >> 16);
+  for (int b0 = 0; b0 < kPieces; b0 += kBatch) {
+    i32x4 v[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int p = tid + (b0 + q) * kMgThreads;
+      const int i = p / (kMgCols / 8);
+      const int kk = (p % (kMgCols / 8)) * 8;
+      const uint32_t off = i < rank ? (uint32_t)(i * K + k0 + kk) * 2u : kOob;
+      v[q] = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)off, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int p = tid + (b0 + q) * kMgThreads;
+      const int i = p / (kMgCols / 8);
+      const int kk = (p % (kMgCols / 8)) * 8;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        at[(kk + 2 * e) * AP + i] = (uint16_t)((uint32_t)v[q][e] & 0xffffu);
+        at[(kk + 2 * e + 1) * AP + i] = (uint16_t)((uint32_t)v[q][e] >> 16);
+      }
     }
   }
   __syncthreads();
@@ -510,20 +535,43 @@ __global__ __launch_bounds__(kMgThreads) void dequant_merge_kernel(
   for (int tt = 0; tt < kMgTiles; ++tt) {
     const int cur = tt & 1;
     if (tt + 1 < kMgTiles) { load_tile(cur ^ 1, tt + 1); }
-    // 2. D[4 (lane / 16) + t][16 kb + lane % 16] of the wave's rows
+    // 2. D[4 (lane / 16) + t][16 kb + lane % 16] of the wave's rows: the
+    // eight blocks' accumulators are independent, so the rank chunks run
+    // outermost and consecutive MFMAs never wait on each other
+    // A's fragments for rank chunk c + 1 are read from LDS while chunk c's
+    // MFMAs run (the order held by scheduling barriers): read just before
+    // its MFMA, each fragment's LDS latency stalled the wave.
+    constexpr int KB = kMgCols / 16;
+    f32x4 d[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) { d[kb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f}; }
+    i32x4 af[2][KB];
+    auto read_a = [&](int slot, int c) {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        af[slot][kb] = *(const i32x4*)(at + (16 * kb + (lane & 15)) * AP + 32 * c +
+                                       8 * (lane >> 4));
+      }
+    };
+    read_a(0, 0);
+#pragma unroll
+    for (int c = 0; c < R / 32; ++c) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (c + 1 < R / 32) { read_a((c + 1) & 1, c + 1); }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        d[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, bf[cur][c]),
+                                                        __builtin_bit_cast(bf16x8, af[c & 1][kb]),
+                                                        d[kb], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kb = 0; kb < kMgCols / 16; ++kb) {
-      f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int c = 0; c < R / 32; ++c) {
-        const i32x4 af = *(const i32x4*)(at + (16 * kb + (lane & 15)) * AP + 32 * c +
-                                         8 * (lane >> 4));
-        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, bf[cur][c]),
-                                                    __builtin_bit_cast(bf16x8, af), d, 0, 0, 0);
-      }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        dw[(4 * (lane >> 4) + t) * kMgDp + 16 * kb + (lane & 15)] = d[t];
+        dw[(4 * (lane >> 4) + t) * kMgDp + 16 * kb + (lane & 15)] = d[kb][t];
       }
     }
     // 3. W' = bf16(fma(s, code, z) + D), one 16-byte store per run
@@ -552,33 +600,38 @@ __global__ __launch_bounds__(kMgThreads) void dequant_merge_kernel(
 
 }  // namespace
 
-// The merge takes w8 codes, K % 128 == 0, rank % 8 == 0 up to 64, A and B
+// The merge takes w8 codes, K % 128 == 0, rank up to kMgMaxRank, B's row
+// stride ldb a multiple of 8 (its columns from rank to ldb zero), A and B
 // 16-byte aligned and every operand under 2 GiB (32-bit buffer offsets).
-bool dequant_merge_takes(int bits, int N, int K, int rank, const void* a, const void* b)
+bool dequant_merge_takes(int bits, int N, int K, int rank, int ldb, const void* a, const void* b)
 {
   const size_t lim = (size_t)1 << 31;
-  return bits == 8 && N > 0 && K > 0 && K % kMgCols == 0 && rank > 0 && rank <= 64 &&
-         rank % 8 == 0 && ((uintptr_t)a & 15u) == 0 && ((uintptr_t)b & 15u) == 0 &&
-         (size_t)rank * K * 2 < lim && (size_t)N * rank * 2 < lim && (size_t)N * K * 2 < lim;
+  return bits == 8 && N > 0 && K > 0 && K % kMgCols == 0 && rank > 0 && rank <= kMgMaxRank &&
+         ldb >= rank && ldb % 8 == 0 && ((uintptr_t)a & 15u) == 0 &&
+         ((uintptr_t)b & 15u) == 0 && (size_t)rank * K * 2 < lim && (size_t)N * ldb * 2 < lim &&
+         (size_t)N * K * 2 < lim;
 }
 
 hipError_t launch_dequant_merge(const uint8_t* codes, const uint16_t* scales,
                                 const uint16_t* qbias, int group, const uint16_t* a,
-                                const uint16_t* b, int rank, uint16_t* out, int N, int K,
-                                hipStream_t stream)
+                                const uint16_t* b, int rank, int ldb, uint16_t* out, int N,
+                                int K, hipStream_t stream)
 {
-  if (!dequant_merge_takes(8, N, K, rank, a, b) || (group != 32 && group != 64)) {
+  if (!dequant_merge_takes(8, N, K, rank, ldb, a, b) || (group != 32 && group != 64)) {
     return hipErrorInvalidValue;
   }
   const int gshift = group == 64 ? 6 : 5;
   const int rows = kMgRows * kMgTiles;
   const dim3 grid((unsigned)(K / kMgCols), (unsigned)((N + rows - 1) / rows));
+  auto go = [&](auto r) {
+    constexpr int R = decltype(r)::value;
+    dequant_merge_kernel<R><<<grid, kMgThreads, 0, stream>>>(codes, scales, qbias, gshift,
+                                                             K / group, a, b, rank, ldb, out, N, K);
+  };
   if (rank <= 32) {
-    dequant_merge_kernel<32><<<grid, kMgThreads, 0, stream>>>(codes, scales, qbias, gshift,
-                                                              K / group, a, b, rank, out, N, K);
+    go(std::integral_constant<int, 32>{});
   } else {
-    dequant_merge_kernel<64><<<grid, kMgThreads, 0, stream>>>(codes, scales, qbias, gshift,
-                                                              K / group, a, b, rank, out, N, K);
+    go(std::integral_constant<int, 64>{});
   }
   return hipGetLastError();
 }
