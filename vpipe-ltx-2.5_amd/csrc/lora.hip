@@ -417,7 +417,7 @@ __global__ void lora_pad_kernel(const uint16_t* __restrict__ src, int rows, int 
 }
 
 // ---- the adapter merged into the dequant-once expansion ----------------
-//   W'[n][k] = bf16(fma(scale, code, bias) + sum_{i < rank} B[n][i] A[i][k])
+//   W'[n][k] = bf16(fma(scale, code, zero point) + sum_{i < rank} B[n][i] A[i][k])
 // The linear then runs over W' at its own K. (x . A^T) . B^T = x . (B . A)^T,
 // so this is the adapter of the reference's lora_add
 // (src/ltx25-metal-ops.cc:989-1004) applied to the weight instead of the
