@@ -484,9 +484,11 @@ tall_kernel(TallParams p)
   // The epilogue's choices are made once, outside the unrolled staging loop:
   // a runtime test per output became a scalar branch per output, which kept
   // the scheduler from interleaving outputs (and made it rematerialize the
-  // GELU's constants per output). Without a bias the add of +0 is skipped:
-  // an accumulator is never -0 (it starts at +0, or at y_in, and x + (-x)
-  // rounds to +0), so the bits are the same.
+  // GELU's constants per output). Without a bias no +0 is added. An
+  // accumulator that starts at +0 is never -0 (x + (-x) rounds to +0), so
+  // those bits are unchanged; one seeded from y_in = -0 whose products are
+  // all -0 stays -0, as the reference's accumulate into y (lora_mma_'s
+  // second GEMM, src/ltx25-metal-ops.cc:938-987) adds no bias either.
   auto stage_tile = [&](auto gelu, auto biased) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
