@@ -736,6 +736,9 @@ def bench_lora(pkg, torch, steps, warmup):
         lin = ab["linear"]["best_ms"]
         out[f"rank{rank}_with_linear"] = {
             "fold_taken": pkg.lora_fold_takes(M, K, N, rank, 8),
+            # w8 codes, K % 128 == 0 and an aligned A here: merged into the expansion up to
+            # rank 64 (ltx25_linear_q_lora's rule), extra K above
+            "fold_form": "merged into the expansion" if rank <= 64 else "extra K",
             "linear_us": lin * 1e3,
             "fold_us": ab["fold"]["best_ms"] * 1e3,
             "sequence_us": ab["sequence"]["best_ms"] * 1e3,
