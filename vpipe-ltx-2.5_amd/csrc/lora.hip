@@ -535,12 +535,12 @@ __global__ __launch_bounds__(kMgThreads) void dequant_merge_kernel(
   for (int tt = 0; tt < kMgTiles; ++tt) {
     const int cur = tt & 1;
     if (tt + 1 < kMgTiles) { load_tile(cur ^ 1, tt + 1); }
-    // 2. D[4 (lane / 16) + t][16 kb + lane % 16] of the wave's rows: the
+    // 2. D[4 (lane / 16) + t][16 kb + lane % 16] of the wave's rows. The
     // eight blocks' accumulators are independent, so the rank chunks run
-    // outermost and consecutive MFMAs never wait on each other
-    // A's fragments for rank chunk c + 1 are read from LDS while chunk c's
-    // MFMAs run (the order held by scheduling barriers): read just before
-    // its MFMA, each fragment's LDS latency stalled the wave.
+    // outermost and consecutive MFMAs never wait on each other; A's
+    // fragments for chunk c + 1 are read from LDS while chunk c's MFMAs run
+    // (the order held by scheduling barriers: read just before its MFMA,
+    // each fragment's LDS latency stalled the wave).
     constexpr int KB = kMgCols / 16;
     f32x4 d[KB];
 #pragma unroll
