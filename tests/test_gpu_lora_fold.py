@@ -260,3 +260,36 @@ def test_fold_random_shapes(pkg, dev, M, K, N, rank, bits, group, bias_kind, epi
     ref = _oracle_rows(xb, wb, ab, bb, bias, epi, np.arange(M))
     assert orc.max_rel(got, ref) <= MAX_REL
     assert orc.rel_l2(got, ref) < REL_L2_ORACLE
+
+
+def test_fold_forms_agree_and_are_deterministic(pkg, dev):
+    """The same adapter through both fold forms: merged into the expansion (A aligned) and as
+    extra K (the same A one element into its storage, which the merge does not take). The two
+    differ only in where they round (the weight, or r): each is within the oracle's rel-L2 bar,
+    so by the triangle inequality they are within twice it of each other; and each call repeats
+    bit for bit."""
+    M, K, N, rank = 1024, 1024, 768, 32
+    pkg.set_dequant_once(pkg.DEQUANT_ONCE_ON)
+    xb, qw, wb, ab, bb, bias = _operands(pkg, M, K, N, rank, 8, 64, "f32", 11)
+    xd, bbd, bd = dev_bf16(xb), dev_bf16(bb), _bias_dev(bias, "f32")
+    ad = dev_bf16(ab)
+    store = torch.empty((rank * K + 8,), dtype=torch.bfloat16, device="cuda")
+    ad_off = store[1:1 + rank * K].view(rank, K)
+    ad_off.copy_(ad)
+    outs = {}
+    for name, a_in in (("merged", ad), ("extra K", ad_off)):
+        runs = []
+        for _ in range(2):
+            y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+            say(f"lora fold forms: {name}")
+            pkg.linear_q_lora(xd, qw, bd, a_in, bbd, rank, y, M, K, N, 1)
+            torch.cuda.synchronize()
+            runs.append(host_bits(y))
+        assert np.array_equal(runs[0], runs[1]), name
+        outs[name] = orc.bf16_to_f32(runs[0])
+    assert not np.array_equal(outs["merged"], outs["extra K"])   # two different roundings
+    ref = _oracle_rows(xb, wb, ab, bb, bias, 1, np.arange(M))
+    for name, got in outs.items():
+        assert orc.max_rel(got, ref) <= MAX_REL, name
+        assert orc.rel_l2(got, ref) < REL_L2_ORACLE, name
+    assert orc.rel_l2(outs["merged"], outs["extra K"]) < 2 * REL_L2_ORACLE
