@@ -586,60 +586,69 @@ qgemm_kernel(KParams p)
     constexpr int CPR = BN / 8;   // 16-byte chunks per row
     const bool vec_rows = (p.N & 7) == 0;
     __syncthreads();   // every wave is done reading the operand tiles
+    // the GELU choice made once, outside the unrolled staging loop (a
+    // runtime test inside it became a scalar branch per group of outputs)
+    auto stage_tile = [&](auto gelu) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      float bv[4][4];
-      float swv[4][4];   // int8 GEMM: per-column weight scales
+      for (int j = 0; j < FN; ++j) {
+        float bv[4][4];
+        float swv[4][4];   // int8 GEMM: per-column weight scales
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+        for (int g = 0; g < 4; ++g) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int n = n0 + wn * WTN + j * 32 + g * 8 + lcol + t;
-          const int c = wn * WTN + j * 32 + g * 8 + lcol + t;
-          bv[g][t] = n < p.N ? lds_ep[c] : 0.0f;
-          swv[g][t] = I8 && n < p.N ? lds_ep[BN + c] : 0.0f;
+          for (int t = 0; t < 4; ++t) {
+            const int n = n0 + wn * WTN + j * 32 + g * 8 + lcol + t;
+            const int c = wn * WTN + j * 32 + g * 8 + lcol + t;
+            bv[g][t] = n < p.N ? lds_ep[c] : 0.0f;
+            swv[g][t] = I8 && n < p.N ? lds_ep[BN + c] : 0.0f;
+          }
         }
-      }
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int r = wm * WTM + i * 32 + lrow;
-        uint16_t* srow = r < BM / 2 ? stage_lo + r * EP : stage_hi + (r - BM / 2) * EP;
-        const int m = m0 + r;
-        const float sxm = I8 && m < p.M ? lds_ep[2 * BN + r] : 0.0f;
-        if constexpr (I8) {
-          // the raw int32 accumulators, when asked for (bit-exact checks)
-          if (p.acc_out != nullptr && m < p.M) {
-            int32_t* arow = p.acc_out + (size_t)m * p.N;
+        for (int i = 0; i < FM; ++i) {
+          const int r = wm * WTM + i * 32 + lrow;
+          uint16_t* srow = r < BM / 2 ? stage_lo + r * EP : stage_hi + (r - BM / 2) * EP;
+          const int m = m0 + r;
+          const float sxm = I8 && m < p.M ? lds_ep[2 * BN + r] : 0.0f;
+          if constexpr (I8) {
+            // the raw int32 accumulators, when asked for (bit-exact checks)
+            if (p.acc_out != nullptr && m < p.M) {
+              int32_t* arow = p.acc_out + (size_t)m * p.N;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const int n = n0 + wn * WTN + j * 32 + g * 8 + lcol;
+              for (int g = 0; g < 4; ++g) {
+                const int n = n0 + wn * WTN + j * 32 + g * 8 + lcol;
 #pragma unroll
-              for (int t = 0; t < 4; ++t) {
-                if (n + t < p.N) { arow[n + t] = acc[i][j][4 * g + t]; }
+                for (int t = 0; t < 4; ++t) {
+                  if (n + t < p.N) { arow[n + t] = acc[i][j][4 * g + t]; }
+                }
               }
             }
           }
-        }
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float v[4];
+          for (int g = 0; g < 4; ++g) {
+            float v[4];
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            if constexpr (I8) {
-              // y = bf16(fma(float(acc), sx[m] * sw[n], bias[n])), that order
-              v[t] = fmaf((float)acc[i][j][4 * g + t], sxm * swv[g][t], bv[g][t]);
-            } else {
-              v[t] = acc[i][j][4 * g + t] + bv[g][t];
+            for (int t = 0; t < 4; ++t) {
+              if constexpr (I8) {
+                // y = bf16(fma(float(acc), sx[m] * sw[n], bias[n])), that order
+                v[t] = fmaf((float)acc[i][j][4 * g + t], sxm * swv[g][t], bv[g][t]);
+              } else {
+                v[t] = acc[i][j][4 * g + t] + bv[g][t];
+              }
             }
-          }
-          if (p.epilogue == kEpiGelu) {
+            if constexpr (decltype(gelu)::value) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) { v[t] = gelu_tanh(v[t]); }
+              for (int t = 0; t < 4; ++t) { v[t] = gelu_tanh(v[t]); }
+            }
+            *(uint2*)(srow + wn * WTN + j * 32 + g * 8 + lcol) =
+                make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
           }
-          *(uint2*)(srow + wn * WTN + j * 32 + g * 8 + lcol) =
-              make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
         }
       }
+    };
+    if (p.epilogue == kEpiGelu) {
+      stage_tile(std::true_type{});
+    } else {
+      stage_tile(std::false_type{});
     }
     __syncthreads();
 #pragma unroll 4
