@@ -23,21 +23,37 @@ constexpr int kRowsPerBlock = kThreads / 64;   // one wave per row
 constexpr int kCacheChunks = 16;
 
 // q = clamp(rint(v / s), -127, 127) with v / s correctly rounded, given
-// rs = 1 / s rounded. t = v * rs is within 2^-24 |v / s| (1 + 2^-24) of the
-// quotient, i.e. within 2^-15 for |t| < 256; so rint(t) = rint(v / s)
-// unless t lies within 2^-13 of a half-integer. Those values, and any t that
-// is not a finite number below 256 (s tiny, v or s not finite), take the
-// division itself.
-__device__ __forceinline__ uint32_t q8(float v, float s, float rs)
+// rs = 1 / s rounded, for four values packed low byte first. t = v * rs is
+// within 2^-24 |v / s| (1 + 2^-24) of the quotient, i.e. within 2^-15 for
+// |t| < 256; so rint(t) = rint(v / s) unless t lies within 2^-13 of a
+// half-integer. Those values, and any t that is not a finite number below
+// 256 (s tiny, v or s not finite), take the division itself. The test for
+// that fallback is made once for the four values (a test per value was a
+// branch per value around the rarely taken division); s <= 0 gives 0.
+__device__ __forceinline__ uint32_t q8x4(const float* v, float s, float rs)
 {
-  float r = 0.0f;
-  if (s > 0.0f) {
-    const float t = v * rs;
-    r = rintf(t);
-    if (!(fabsf(t) < 256.0f) || fabsf(t - r) > 0.5f - 0x1p-13f) { r = rintf(v / s); }
-    r = fminf(fmaxf(r, -127.0f), 127.0f);
+  if (!(s > 0.0f)) { return 0u; }
+  float r[4];
+  int slow = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float t = v[j] * rs;
+    r[j] = rintf(t);
+    slow |= (int)!(fabsf(t) < 256.0f) | (int)(fabsf(t - r[j]) > 0.5f - 0x1p-13f);
   }
-  return (uint32_t)(int)r & 0xffu;
+  if (slow) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float t = v[j] * rs;
+      if (!(fabsf(t) < 256.0f) || fabsf(t - r[j]) > 0.5f - 0x1p-13f) { r[j] = rintf(v[j] / s); }
+    }
+  }
+  uint32_t out = 0u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    out |= ((uint32_t)(int)fminf(fmaxf(r[j], -127.0f), 127.0f) & 0xffu) << (8 * j);
+  }
+  return out;
 }
 
 __device__ __forceinline__ float wave_absmax(float amax)
@@ -90,13 +106,10 @@ i8_quantize_rows_kernel(const uint16_t* x, int8_t* q, float* scale, int M, int K
   if (lane == 0) { scale[m] = s; }
   auto quant8 = [&](const uint4& v, int i) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    uint32_t packed[2] = {0u, 0u};
+    float f[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint16_t h = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
-      packed[j >> 2] |= q8(bf16_to_f32(h), s, rs) << (8 * (j & 3));
-    }
-    *(uint2*)(qr + (size_t)i * 8) = make_uint2(packed[0], packed[1]);
+    for (int j = 0; j < 8; ++j) { f[j] = bf16_to_f32((uint16_t)(w[j >> 1] >> (16 * (j & 1)))); }
+    *(uint2*)(qr + (size_t)i * 8) = make_uint2(q8x4(f, s, rs), q8x4(f + 4, s, rs));
   };
 #pragma unroll
   for (int c = 0; c < kCacheChunks; ++c) {
@@ -174,10 +187,7 @@ i8_quantize_qweight_kernel(const uint8_t* codes, const uint16_t* scales,
     dequant(c, i, v);
     uint32_t packed[CPC / 4];
 #pragma unroll
-    for (int t = 0; t < CPC / 4; ++t) {
-      packed[t] = q8(v[4 * t], s, rs) | (q8(v[4 * t + 1], s, rs) << 8) |
-                  (q8(v[4 * t + 2], s, rs) << 16) | (q8(v[4 * t + 3], s, rs) << 24);
-    }
+    for (int t = 0; t < CPC / 4; ++t) { packed[t] = q8x4(v + 4 * t, s, rs); }
 #pragma unroll
     for (int t = 0; t < CPC / 16; ++t) {
       *(uint4*)(qr + (size_t)i * CPC + 16 * t) =
