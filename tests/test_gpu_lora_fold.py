@@ -293,3 +293,44 @@ def test_fold_forms_agree_and_are_deterministic(pkg, dev):
         assert orc.max_rel(got, ref) <= MAX_REL, name
         assert orc.rel_l2(got, ref) < REL_L2_ORACLE, name
     assert orc.rel_l2(outs["merged"], outs["extra K"]) < 2 * REL_L2_ORACLE
+
+
+# rank, K, bits, group, whether the merge into the expansion takes
+BOUNDARY = [
+    (64, 512, 8, 64, True),     # the largest rank the merge takes
+    (65, 512, 8, 64, False),    # one above it: extra K
+    (64, 512, 8, 32, True),
+    (32, 576, 8, 64, False),    # K % 128 != 0: extra K
+    (32, 512, 4, 64, False),    # w4 codes: extra K
+]
+
+
+@pytest.mark.parametrize("rank,K,bits,group,merges", BOUNDARY,
+                         ids=[f"r{c[0]}-K{c[1]}-w{c[2]}g{c[3]}" for c in BOUNDARY])
+def test_merge_boundary(pkg, dev, rank, K, bits, group, merges):
+    """Where the merge takes, an aligned A (merged) and the same A one element into its
+    storage (extra K: the merge needs an aligned A) round in different places, so the two
+    outputs differ; where it does not take, both calls run the extra-K form and agree bit for
+    bit. Each output is within the oracle's bars."""
+    M, N = 256, 256
+    pkg.set_dequant_once(pkg.DEQUANT_ONCE_ON)
+    assert pkg.lora_fold_takes(M, K, N, rank, bits)
+    xb, qw, wb, ab, bb, bias = _operands(pkg, M, K, N, rank, bits, group, "bf16", rank + K)
+    xd, bbd, bd = dev_bf16(xb), dev_bf16(bb), _bias_dev(bias, "bf16")
+    ad = dev_bf16(ab)
+    store = torch.empty((rank * K + 8,), dtype=torch.bfloat16, device="cuda")
+    ad_off = store[1:1 + rank * K].view(rank, K)
+    ad_off.copy_(ad)
+    ref = _oracle_rows(xb, wb, ab, bb, bias, 1, np.arange(M))
+    outs = []
+    for a_in in (ad, ad_off):
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        say(f"lora merge boundary: rank={rank} K={K} w{bits}g{group} "
+            f"A {'aligned' if a_in is ad else 'one element in'}")
+        pkg.linear_q_lora(xd, qw, bd, a_in, bbd, rank, y, M, K, N, 1)
+        torch.cuda.synchronize()
+        got = host_bits(y)
+        assert orc.max_rel(orc.bf16_to_f32(got), ref) <= MAX_REL
+        assert orc.rel_l2(orc.bf16_to_f32(got), ref) < REL_L2_ORACLE
+        outs.append(got)
+    assert np.array_equal(outs[0], outs[1]) != merges
